@@ -1,0 +1,147 @@
+/*
+ * moa_ops.h -- C ABI of the MI355X (gfx950) decoder-layer hot path.
+ *
+ * Drop-in for the three Stage-1 operators of the reference crate
+ * (furiosa-opt-gemma4-12B, "FO/" below). Each entry point keeps the argument order and
+ * meaning of the reference's `#[device] fn` in FO/src/ops.rs, with the `device` handle
+ * replaced by a trailing (M, stream) pair:
+ *   - every tensor is a caller-owned device pointer (hipMalloc'd); the library never
+ *     allocates per call (one per-device scratch block is made on first use or by moa_init);
+ *   - `&mut` tensors of the reference (k_cache, v_cache, q_out, residual) are written in place;
+ *   - bf16 tensors are raw uint16 bit patterns; E4M3FN/E2M1/E8M0 are uint8 codes;
+ *   - M is the number of token rows (the reference processes exactly one, M = 1);
+ *   - stream is a hipStream_t (NULL = the null stream); all work is ordered on it and the
+ *     call returns without synchronising. Calls on one device must be issued from one
+ *     stream at a time: the per-device scratch is shared.
+ * Pointers must be 16-byte aligned except per-channel scales (natural alignment).
+ *
+ * Return value: MOA_SUCCESS or a negative MOA_ERROR_* code; moa_last_error_string() gives
+ * the reason. Invalid arguments are rejected before anything is launched. Device-resident
+ * offsets are validated by the kernel: an out-of-range offset writes nothing and raises a
+ * bit read back by moa_device_errors().
+ *
+ * Shapes (FO/src/axes.rs:3-29): H=3840 hidden, L=15360 intermediate, 8 KV heads x 2 query
+ * heads x 256 head_dim (Q=4096, K/V=2048), ring cache T=1024 slots, RoPE table E=32768 rows.
+ */
+#ifndef MOA_OPS_H
+#define MOA_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOA_SUCCESS 0
+#define MOA_ERROR_INVALID_VALUE (-1) /* null pointer, bad M or shape */
+#define MOA_ERROR_MISALIGNED (-2)    /* pointer not 16-byte aligned */
+#define MOA_ERROR_HIP (-3)           /* a HIP runtime call failed */
+#define MOA_ERROR_NO_DEVICE (-4)     /* no usable gfx950 device */
+#define MOA_ERROR_DEVICE_STATE (-5)  /* a kernel flagged a bad device-resident argument */
+
+#define MOA_DEVERR_ROPE_OFFSET 1u /* rope_offset not a multiple of 512 or past the table */
+#define MOA_DEVERR_KV_OFFSET 2u   /* kv_offset not a multiple of 4096 or past the ring */
+
+/* Library version string. */
+const char* moa_version(void);
+
+/* Reason for the last non-zero return on this thread. */
+const char* moa_last_error_string(void);
+
+/* Allocates the per-device scratch of `device` (also done lazily by the first call). Call it
+ * before capturing calls into a HIP graph. */
+int moa_init(int device);
+
+/* Synchronises `stream`, returns the OR of device-side error bits raised since the last call
+ * (MOA_DEVERR_*) in *bits, and clears them. */
+int moa_device_errors(void* stream, uint32_t* bits);
+
+/* ops::sliding_project_qkv -- FO/src/ops.rs:37-76.
+ * x bf16 [M,3840]; q_weight E4M3 [4096,3840]; k_weight, v_weight E4M3 [2048,3840] (row =
+ * output channel); *_weight_scale f32 per output channel; input_rms_weight bf16 [3840];
+ * q_rms_weight, k_rms_weight bf16 [256]; kv_offset, rope_offset: device int32 BYTE offsets
+ * for row 0 (slot*8*256*2 and pos*256*2, FO/src/bin/test_kernels.rs:520-527); row m uses
+ * table row rope_offset/512+m and ring slot (kv_offset/4096+m) mod 1024; cos, sin bf16
+ * [32768,256] (sin with its low half negated, FO/scripts/generate_references.py:200-210);
+ * k_cache, v_cache bf16 [1024,8,256] (only the addressed slots are written); q_out bf16
+ * [M,8,2,256]. */
+int moa_sliding_project_qkv(const uint16_t* x, const uint8_t* q_weight, const uint8_t* k_weight,
+                            const uint8_t* v_weight, const float* q_weight_scale,
+                            const float* k_weight_scale, const float* v_weight_scale,
+                            const uint16_t* input_rms_weight, const uint16_t* q_rms_weight,
+                            const uint16_t* k_rms_weight, const int32_t* kv_offset,
+                            const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
+                            uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M,
+                            void* stream);
+
+/* Same with bf16 per-channel scales, the exact operand types of FO/src/ops.rs:44-46. */
+int moa_sliding_project_qkv_bf16_scales(
+    const uint16_t* x, const uint8_t* q_weight, const uint8_t* k_weight, const uint8_t* v_weight,
+    const uint16_t* q_weight_scale, const uint16_t* k_weight_scale, const uint16_t* v_weight_scale,
+    const uint16_t* input_rms_weight, const uint16_t* q_rms_weight, const uint16_t* k_rms_weight,
+    const int32_t* kv_offset, const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
+    uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M, void* stream);
+
+/* ops::sliding_attention_output -- FO/src/ops.rs:130-146.
+ * x bf16 [M,4096] (= [M,8,2,256]); post_attn_rms_weight bf16 [3840]; o_weight E4M3
+ * [3840,4096]; o_weight_scale f32 [3840]; residual bf16 [M,3840], updated in place:
+ * residual = bf16(residual + RMSNorm(bf16((x.W^T) * scale), post_attn_rms_weight)). */
+int moa_sliding_attention_output(const uint16_t* x, const uint16_t* post_attn_rms_weight,
+                                 const uint8_t* o_weight, const float* o_weight_scale,
+                                 uint16_t* residual, int M, void* stream);
+
+/* Same with bf16 scales (FO/src/ops.rs:136). */
+int moa_sliding_attention_output_bf16_scales(const uint16_t* x, const uint16_t* post_attn_rms_weight,
+                                             const uint8_t* o_weight, const uint16_t* o_weight_scale,
+                                             uint16_t* residual, int M, void* stream);
+
+/* ops::decoder_feedforward -- FO/src/ops.rs:201-239, NVFP4 weights exactly as the reference:
+ * *_weight_packed E2M1 two per byte, low nibble first (up/gate [15360,1920], down [3840,7680]);
+ * *_weight_scale E4M3 per 16 K-elements (up/gate [15360,240], down [3840,960]);
+ * *_global_scale device f32 [1] holding the RECIPROCAL global scale (FO/src/host/load.rs:170-190);
+ * pre/post_ff_rms_weight bf16 [3840]; layer_scalar bf16 [8] (element 0 used);
+ * residual bf16 [M,3840] updated in place. */
+int moa_decoder_feedforward(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                            const uint8_t* up_weight_packed, const uint8_t* gate_weight_packed,
+                            const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+                            const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale,
+                            const float* up_global_scale, const float* gate_global_scale,
+                            const float* down_global_scale, const uint16_t* post_ff_rms_weight,
+                            const uint16_t* layer_scalar, int M, void* stream);
+
+/* GeGLU FFN with FP8 E4M3 weights and per-output-channel f32 scales (no counterpart in the
+ * reference's weights; same operator contract as FO/src/ops.rs:201-239 with each projection
+ * computed as FO/scripts/generate_references.py:265-274 scaled_projection).
+ * up, gate E4M3 [15360,3840]; down E4M3 [3840,15360]; scales f32 [15360],[15360],[3840].
+ * post_ff_rms_weight and layer_scalar may be NULL (skip the post norm / the gate). */
+int moa_decoder_feedforward_fp8(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                                const uint8_t* up_weight, const uint8_t* gate_weight,
+                                const uint8_t* down_weight, const float* up_weight_scale,
+                                const float* gate_weight_scale, const float* down_weight_scale,
+                                const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
+                                int M, void* stream);
+
+/* GeGLU FFN with MXFP4 weights: E2M1 two per byte (as NVFP4) with E8M0 scales per 32
+ * K-elements (up/gate [15360,120], down [3840,480]); no global scale. Same contract
+ * otherwise; post_ff_rms_weight and layer_scalar may be NULL. */
+int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                                  const uint8_t* up_weight_packed, const uint8_t* gate_weight_packed,
+                                  const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+                                  const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale,
+                                  const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
+                                  int M, void* stream);
+
+/* The FP8 projection alone -- FO/scripts/generate_references.py:265-274 scaled_projection:
+ * out[m,n] = bf16((x[m,:] . dec(w[n,:])) * scale[n]). x bf16 [M,K], w E4M3 [N,K], scale f32
+ * [N], out bf16 [M,N]; K % 16 == 0. */
+int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* scale, uint16_t* out,
+                              int M, int N, int K, void* stream);
+
+/* Test support: decodes every E4M3 code, E2M1 byte, E8M0 code and bf16 GeLU input with the
+ * kernels' own device helpers into out (device uint32 [66560]; layout in moa_decode.hip). */
+int moa_format_selftest(uint32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

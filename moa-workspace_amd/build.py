@@ -1,0 +1,53 @@
+#!/usr/bin/env python3
+"""Build libmoa_gfx950.so in-tree with hipcc (cross-compiles without a GPU).
+
+    python moa-workspace_amd/build.py [--verbose]
+
+Flags:
+  --offload-arch=gfx950                  MI355X only
+  -ffp-contract=off                      every multiply/add rounds on its own, as the
+                                         reference's torch ops do; kernels call fmaf()
+                                         explicitly where the product is exact
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                         no packed-FP32 VALU instructions
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libmoa_gfx950.so"
+SOURCES = ["moa_api.hip", "moa_decode.hip", "moa_chunk.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def build(verbose: bool = False) -> Path:
+    srcs = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, "-o", str(tmp), *srcs]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    msgs = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{msgs}")
+    if verbose and msgs.strip():
+        print(msgs)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="--verbose" in sys.argv))

@@ -1,0 +1,294 @@
+// moa_api.hip -- the C ABI (include/moa_ops.h): argument validation, per-device scratch,
+// and dispatch to the decode (small M) or chunk (large M) kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/moa_ops.h"
+#include "moa_internal.h"
+
+namespace moa {
+namespace {
+
+thread_local std::string g_error;
+std::mutex g_ctx_mutex;
+constexpr int kMaxDevices = 64;
+DevCtx g_ctx[kMaxDevices];
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(MOA_ERROR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+DevCtx* device_context(hipError_t* err) {
+    int dev = 0;
+    *err = hipGetDevice(&dev);
+    if (*err != hipSuccess) return nullptr;
+    if (dev < 0 || dev >= kMaxDevices) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_ctx_mutex);
+    DevCtx& c = g_ctx[dev];
+    if (c.base) return &c;
+    size_t off = 0;
+    auto carve = [&](size_t bytes) { size_t at = off; off = align_up(off + bytes, 256); return at; };
+    const size_t t_tickets = carve(sizeof(uint32_t) * kTicketCount);
+    const size_t t_err = carve(sizeof(uint32_t) * 4);
+    const size_t t_raw = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * (kQs + 2 * kPs));
+    const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);
+    const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
+    const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
+    void* base = nullptr;
+    *err = hipMalloc(&base, off);
+    if (*err != hipSuccess) return nullptr;
+    *err = hipMemset(base, 0, off);
+    if (*err == hipSuccess) *err = hipDeviceSynchronize();
+    if (*err != hipSuccess) {
+        (void)hipFree(base);
+        return nullptr;
+    }
+    char* b = static_cast<char*>(base);
+    c.device = dev;
+    c.tickets = reinterpret_cast<uint32_t*>(b + t_tickets);
+    c.err = reinterpret_cast<uint32_t*>(b + t_err);
+    c.raw_qkv = reinterpret_cast<uint16_t*>(b + t_raw);
+    c.pbuf = reinterpret_cast<uint16_t*>(b + t_p);
+    c.dbuf = reinterpret_cast<uint16_t*>(b + t_d);
+    c.hbuf = reinterpret_cast<uint16_t*>(b + t_h);
+    c.base = base;
+    return &c;
+}
+
+}  // namespace moa
+
+using namespace moa;
+
+namespace {
+
+struct Check {
+    int code = MOA_SUCCESS;
+    // Required pointer with the given alignment.
+    Check& ptr(const void* p, const char* name, size_t align = 16) {
+        if (code) return *this;
+        if (!p) { code = fail(MOA_ERROR_INVALID_VALUE, std::string(name) + " is NULL"); return *this; }
+        if (reinterpret_cast<uintptr_t>(p) % align) {
+            code = fail(MOA_ERROR_MISALIGNED, std::string(name) + " is not " + std::to_string(align) + "-byte aligned");
+        }
+        return *this;
+    }
+    // Optional pointer: NULL allowed.
+    Check& opt(const void* p, const char* name, size_t align = 16) {
+        if (code || !p) return *this;
+        return ptr(p, name, align);
+    }
+    Check& rows(int M) {
+        if (code) return *this;
+        if (M < 1 || M > (1 << 20)) code = fail(MOA_ERROR_INVALID_VALUE, "M must be in [1, 2^20], got " + std::to_string(M));
+        return *this;
+    }
+};
+
+DevCtx* ctx_or_fail(int* code) {
+    hipError_t e;
+    DevCtx* c = device_context(&e);
+    if (!c) *code = hip_fail(e, "allocating the per-device scratch");
+    return c;
+}
+
+int finish(hipError_t e, const char* what) {
+    if (e != hipSuccess) return hip_fail(e, what);
+    return MOA_SUCCESS;
+}
+
+int qkv_common(const QkvParams& p, int M, void* stream) {
+    Check c;
+    c.ptr(p.x, "x").ptr(p.qw, "q_weight").ptr(p.kw, "k_weight").ptr(p.vw, "v_weight");
+    const size_t sa = p.scale_kind == ScaleKind::F32 ? 4 : 2;
+    c.ptr(p.qs, "q_weight_scale", sa).ptr(p.ks, "k_weight_scale", sa).ptr(p.vs, "v_weight_scale", sa);
+    c.ptr(p.in_rms, "input_rms_weight").ptr(p.q_rms, "q_rms_weight").ptr(p.k_rms, "k_rms_weight");
+    c.ptr(p.kv_off, "kv_offset", 4).ptr(p.rope_off, "rope_offset", 4).ptr(p.cos, "cos").ptr(p.sin, "sin");
+    c.ptr(p.k_cache, "k_cache").ptr(p.v_cache, "v_cache").ptr(p.q_out, "q_out").rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return finish(launch_qkv_decode(p, M, static_cast<hipStream_t>(stream), ctx), "sliding_project_qkv launch");
+}
+
+int o_common(const OParams& p, int M, void* stream) {
+    Check c;
+    c.ptr(p.x, "x").ptr(p.post_rms, "post_attn_rms_weight").ptr(p.ow, "o_weight");
+    c.ptr(p.os, "o_weight_scale", p.scale_kind == ScaleKind::F32 ? 4 : 2).ptr(p.residual, "residual").rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return finish(launch_o_decode(p, M, static_cast<hipStream_t>(stream), ctx), "sliding_attention_output launch");
+}
+
+int ffn_common(const FfnParams& p, int M, void* stream) {
+    Check c;
+    c.ptr(p.residual, "residual").ptr(p.pre_rms, "pre_ff_rms_weight");
+    c.ptr(p.up, "up_weight").ptr(p.gate, "gate_weight").ptr(p.down, "down_weight");
+    if (p.fmt == FfnFormat::FP8) {
+        const size_t sa = p.scale_kind == ScaleKind::F32 ? 4 : 2;
+        c.ptr(p.up_s, "up_weight_scale", sa).ptr(p.gate_s, "gate_weight_scale", sa).ptr(p.down_s, "down_weight_scale", sa);
+    } else {
+        const size_t sa = p.fmt == FfnFormat::NVFP4 ? 2 : 1;
+        c.ptr(p.up_s, "up_weight_scale", sa).ptr(p.gate_s, "gate_weight_scale", sa).ptr(p.down_s, "down_weight_scale", sa);
+    }
+    if (p.fmt == FfnFormat::NVFP4) {
+        c.ptr(p.up_g, "up_global_scale", 4).ptr(p.gate_g, "gate_global_scale", 4).ptr(p.down_g, "down_global_scale", 4);
+        c.ptr(p.post_rms, "post_ff_rms_weight").ptr(p.layer_scalar, "layer_scalar", 2);
+    } else {
+        c.opt(p.post_rms, "post_ff_rms_weight").opt(p.layer_scalar, "layer_scalar", 2);
+    }
+    c.rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return finish(launch_ffn_decode(p, M, static_cast<hipStream_t>(stream), ctx), "decoder_feedforward launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* moa_version(void) { return "moa-gfx950 0.1.0"; }
+
+const char* moa_last_error_string(void) { return g_error.c_str(); }
+
+int moa_init(int device) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(MOA_ERROR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= n) return fail(MOA_ERROR_INVALID_VALUE, "device index out of range");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    int code = MOA_SUCCESS;
+    return ctx_or_fail(&code) ? MOA_SUCCESS : code;
+}
+
+int moa_device_errors(void* stream, uint32_t* bits) {
+    if (!bits) return fail(MOA_ERROR_INVALID_VALUE, "bits is NULL");
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t host = 0;
+    hipError_t e = hipMemcpyAsync(&host, ctx->err, sizeof host, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipMemsetAsync(ctx->err, 0, sizeof(uint32_t), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "reading device error bits");
+    *bits = host;
+    return MOA_SUCCESS;
+}
+
+int moa_sliding_project_qkv(const uint16_t* x, const uint8_t* q_weight, const uint8_t* k_weight,
+                            const uint8_t* v_weight, const float* q_weight_scale,
+                            const float* k_weight_scale, const float* v_weight_scale,
+                            const uint16_t* input_rms_weight, const uint16_t* q_rms_weight,
+                            const uint16_t* k_rms_weight, const int32_t* kv_offset,
+                            const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
+                            uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M, void* stream) {
+    QkvParams p{x, q_weight, k_weight, v_weight, q_weight_scale, k_weight_scale, v_weight_scale, ScaleKind::F32,
+                input_rms_weight, q_rms_weight, k_rms_weight, kv_offset, rope_offset, cos, sin,
+                k_cache, v_cache, q_out};
+    return qkv_common(p, M, stream);
+}
+
+int moa_sliding_project_qkv_bf16_scales(
+    const uint16_t* x, const uint8_t* q_weight, const uint8_t* k_weight, const uint8_t* v_weight,
+    const uint16_t* q_weight_scale, const uint16_t* k_weight_scale, const uint16_t* v_weight_scale,
+    const uint16_t* input_rms_weight, const uint16_t* q_rms_weight, const uint16_t* k_rms_weight,
+    const int32_t* kv_offset, const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
+    uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M, void* stream) {
+    QkvParams p{x, q_weight, k_weight, v_weight, q_weight_scale, k_weight_scale, v_weight_scale, ScaleKind::BF16,
+                input_rms_weight, q_rms_weight, k_rms_weight, kv_offset, rope_offset, cos, sin,
+                k_cache, v_cache, q_out};
+    return qkv_common(p, M, stream);
+}
+
+int moa_sliding_attention_output(const uint16_t* x, const uint16_t* post_attn_rms_weight,
+                                 const uint8_t* o_weight, const float* o_weight_scale,
+                                 uint16_t* residual, int M, void* stream) {
+    OParams p{x, post_attn_rms_weight, o_weight, o_weight_scale, ScaleKind::F32, residual};
+    return o_common(p, M, stream);
+}
+
+int moa_sliding_attention_output_bf16_scales(const uint16_t* x, const uint16_t* post_attn_rms_weight,
+                                             const uint8_t* o_weight, const uint16_t* o_weight_scale,
+                                             uint16_t* residual, int M, void* stream) {
+    OParams p{x, post_attn_rms_weight, o_weight, o_weight_scale, ScaleKind::BF16, residual};
+    return o_common(p, M, stream);
+}
+
+int moa_decoder_feedforward(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                            const uint8_t* up_weight_packed, const uint8_t* gate_weight_packed,
+                            const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+                            const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale,
+                            const float* up_global_scale, const float* gate_global_scale,
+                            const float* down_global_scale, const uint16_t* post_ff_rms_weight,
+                            const uint16_t* layer_scalar, int M, void* stream) {
+    FfnParams p{FfnFormat::NVFP4, residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed,
+                down_weight_packed, up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                up_global_scale, gate_global_scale, down_global_scale, post_ff_rms_weight, layer_scalar};
+    return ffn_common(p, M, stream);
+}
+
+int moa_decoder_feedforward_fp8(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                                const uint8_t* up_weight, const uint8_t* gate_weight,
+                                const uint8_t* down_weight, const float* up_weight_scale,
+                                const float* gate_weight_scale, const float* down_weight_scale,
+                                const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
+                                int M, void* stream) {
+    FfnParams p{FfnFormat::FP8, residual, pre_ff_rms_weight, up_weight, gate_weight, down_weight,
+                up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
+    return ffn_common(p, M, stream);
+}
+
+int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                                  const uint8_t* up_weight_packed, const uint8_t* gate_weight_packed,
+                                  const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+                                  const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale,
+                                  const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
+                                  int M, void* stream) {
+    FfnParams p{FfnFormat::MXFP4, residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed,
+                down_weight_packed, up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
+    return ffn_common(p, M, stream);
+}
+
+int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* scale, uint16_t* out,
+                              int M, int N, int K, void* stream) {
+    Check c;
+    c.ptr(x, "x").ptr(w, "w").ptr(scale, "scale", 4).ptr(out, "out", 2).rows(M);
+    if (c.code) return c.code;
+    if (N < 1 || K < 16 || K % 16) return fail(MOA_ERROR_INVALID_VALUE, "need N >= 1 and K a positive multiple of 16");
+    if (M > 65535) return fail(MOA_ERROR_INVALID_VALUE, "M must be <= 65535 for the projection");
+    ProjParams p{x, w, scale, ScaleKind::F32, out, N, K};
+    return finish(launch_proj_decode(p, M, static_cast<hipStream_t>(stream)), "fp8_scaled_projection launch");
+}
+
+int moa_format_selftest(uint32_t* out, void* stream) {
+    Check c;
+    c.ptr(out, "out", 4);
+    if (c.code) return c.code;
+    return finish(launch_format_selftest(out, static_cast<hipStream_t>(stream)), "format selftest launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,626 @@
+// moa_decode.hip -- decode (small-M, weight-streaming GEMV) kernels for gfx950.
+//
+// At M = 1 the three operators are HBM-bound streams of 1-byte FP8 or packed E2M1 weights.
+// Every kernel here:
+//   * gives each wavefront a few whole weight rows and issues all of their 16-byte loads
+//     first, so a launch keeps ~16-32 KB per wave in flight while the activations are
+//     being prepared;
+//   * stages the (normalised) activation row in LDS as f32 once per workgroup -- barriers
+//     on gfx950 wait only on LDS, so the weight loads stay in flight across them;
+//   * dequantises in registers (v_cvt_pk_f32_fp8 / v_cvt_scalef32_pk_f32_fp4) and
+//     accumulates exact bf16 x fp8/fp4 products in f32 with fmaf;
+//   * reduces each row across the wave with a butterfly (bit-identical in every lane);
+//   * resolves the grid-wide dependency (head RMSNorm + RoPE, post-norm + residual) in the
+//     last-arriving wave, found with a device-scope ticket -- no second launch.
+// blockIdx.y indexes the token row (M <= kMaxDecodeM); rows re-read the same weights, which
+// for small M mostly hit L2/MALL.
+#include "moa_device.h"
+#include "moa_internal.h"
+
+namespace moa {
+namespace {
+
+constexpr int kBlock = 256;  // four waves
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+template <ScaleKind SK>
+__device__ __forceinline__ float load_scale(const void* p, int i) {
+    if constexpr (SK == ScaleKind::F32) return static_cast<const float*>(p)[i];
+    else return bf2f(static_cast<const uint16_t*>(p)[i]);
+}
+
+// Device-scope arrival counter. Returns true (in every lane) for the wave that arrives last
+// among `expected` arrivals; that wave then sees every other wave's stores. The counter
+// resets itself, so consecutive launches on one stream reuse it.
+__device__ __forceinline__ bool wave_arrive(uint32_t* ticket, uint32_t expected) {
+    __threadfence();  // release this wave's global stores (device scope)
+    uint32_t t = 0;
+    if (lane_id() == 0) t = atomicAdd(ticket, 1u);
+    t = __shfl(t, 0, kWave);
+    if (t + 1u != expected) return false;
+    __threadfence();  // acquire the other waves' stores
+    if (lane_id() == 0) atomicExch(ticket, 0u);
+    return true;
+}
+
+// h = RMSNorm(x, w) (gemma4.py:83-89) over kH elements into LDS as f32; w may be null.
+// Whole block. Thread t owns elements [16t, 16t+16) for t < 240.
+__device__ void stage_rmsnorm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                              float* __restrict__ lds, float* __restrict__ red) {
+    const int t = threadIdx.x;
+    const bool act = t < kH / 16;
+    float xv[16];
+    float ss = 0.0f;
+    if (act) {
+        bf16x8_to_f32(ld16(x + t * 16), xv);
+        bf16x8_to_f32(ld16(x + t * 16 + 8), xv + 8);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);  // x*x is exact in f32
+    }
+    ss = wave_sum(ss);
+    if (lane_id() == 0) red[wave_id()] = ss;
+    __syncthreads();
+    const float inv = rms_inverse(((red[0] + red[1]) + red[2]) + red[3], kH);
+    if (act) {
+        float wv[16];
+        if (w) {
+            bf16x8_to_f32(ld16(w + t * 16), wv);
+            bf16x8_to_f32(ld16(w + t * 16 + 8), wv + 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float y = xv[i] * inv;
+            if (w) y = y * wv[i];
+            lds[t * 16 + i] = rbf(y);
+        }
+    }
+    __syncthreads();
+}
+
+// bf16 row of n elements (n % 8 == 0) into LDS as f32. Whole block.
+__device__ void stage_bf16(const uint16_t* __restrict__ x, int n, float* __restrict__ lds) {
+    for (int c = threadIdx.x; c < n / 8; c += kBlock) {
+        float v[8];
+        bf16x8_to_f32(ld16(x + c * 8), v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) lds[c * 8 + i] = v[i];
+    }
+    __syncthreads();
+}
+
+template <int N>
+__device__ __forceinline__ void lds_read(const float* lds, int at, float* out) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(lds + at + i);
+        out[i] = v[0]; out[i + 1] = v[1]; out[i + 2] = v[2]; out[i + 3] = v[3];
+    }
+}
+
+// ------------------------------------------------------------ weight chunks
+// A chunk is the 16 weight bytes one lane loads per row per iteration: 16 FP8 codes or 32
+// E2M1 codes, plus (FP4) the block-scale codes that cover them. Iteration j, lane l covers
+// row bytes [1024 j + 16 l, +16).
+template <FfnFormat F>
+struct Chunk {
+    uint4 q;
+    uint32_t s;
+};
+
+template <FfnFormat F>
+constexpr int elems_per_chunk() { return F == FfnFormat::FP8 ? 16 : 32; }
+
+template <FfnFormat F>
+__device__ __forceinline__ void load_chunk(Chunk<F>& c, const uint8_t* row, const uint8_t* srow,
+                                           int j, int lane, bool valid) {
+    if (!valid) { c.q = make_uint4(0, 0, 0, 0); c.s = 0; return; }
+    c.q = ld_stream(row + j * 1024 + lane * 16);
+    if constexpr (F == FfnFormat::NVFP4)  // block 16: two E4M3 scale codes per chunk
+        c.s = *reinterpret_cast<const uint16_t*>(srow + (j * 64 + lane) * 2);
+    else if constexpr (F == FfnFormat::MXFP4)  // block 32: one E8M0 scale code per chunk
+        c.s = srow[j * 64 + lane];
+    else c.s = 0;
+}
+
+__device__ __forceinline__ float dot_fp8_16(const float* x, const uint4& q, float acc) {
+    float w[16];
+    fp8x4_to_f32(q.x, w); fp8x4_to_f32(q.y, w + 4); fp8x4_to_f32(q.z, w + 8); fp8x4_to_f32(q.w, w + 12);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) acc = fmaf(x[t], w[t], acc);
+    return acc;
+}
+
+__device__ __forceinline__ float dot_fp4_8(const float* x, uint32_t q, float scale, float acc) {
+    float w[8];
+    fp4x8_to_f32(q, scale, w);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc = fmaf(x[t], w[t], acc);
+    return acc;
+}
+
+template <FfnFormat F>
+__device__ __forceinline__ float chunk_dot(const float* x, const Chunk<F>& c, float acc) {
+    if constexpr (F == FfnFormat::FP8) {
+        return dot_fp8_16(x, c.q, acc);
+    } else if constexpr (F == FfnFormat::NVFP4) {
+        // W = e2m1 * e4m3 block scale, exact in f32 (the reference folds it before the
+        // bf16 linear, generate_references.py:398,407).
+        f32x2 s = __builtin_amdgcn_cvt_pk_f32_fp8(c.s, false);
+        acc = dot_fp4_8(x, c.q.x, s[0], acc);
+        acc = dot_fp4_8(x + 8, c.q.y, s[0], acc);
+        acc = dot_fp4_8(x + 16, c.q.z, s[1], acc);
+        return dot_fp4_8(x + 24, c.q.w, s[1], acc);
+    } else {
+        const float s = e8m0_to_f32(c.s);
+        acc = dot_fp4_8(x, c.q.x, s, acc);
+        acc = dot_fp4_8(x + 8, c.q.y, s, acc);
+        acc = dot_fp4_8(x + 16, c.q.z, s, acc);
+        return dot_fp4_8(x + 24, c.q.w, s, acc);
+    }
+}
+
+// Projection commit with the format's rounding rule:
+//   FP8:   bf16(dot * s_row)                 generate_references.py:265-274
+//   NVFP4: bf16(bf16(dot) * inv_global)      generate_references.py:358-372
+//   MXFP4: bf16(dot)
+template <FfnFormat F>
+__device__ __forceinline__ float proj_commit(float dot, float scale) {
+    if constexpr (F == FfnFormat::FP8) return rbf(dot * scale);
+    else if constexpr (F == FfnFormat::NVFP4) return rbf(rbf(dot) * scale);
+    else return rbf(dot);
+}
+
+// out[0:3840] = bf16(bf16(r + N(d)) * ls), N = RMSNorm with w_post or identity when null,
+// ls = layer scalar (skipped when null). One wave; 480 chunks of 8 elements, lane-strided.
+// FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241; oracle generate_references.py:411-413.
+__device__ void wave_post_residual(const uint16_t* __restrict__ d, const uint16_t* __restrict__ w_post,
+                                   uint16_t* __restrict__ r, const uint16_t* __restrict__ ls) {
+    const int lane = lane_id();
+    constexpr int NC = kH / 8;  // 480
+    constexpr int IT = (NC + kWave - 1) / kWave;  // 8
+    float dv[IT][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        const int c = i * kWave + lane;
+        if (c < NC) {
+            bf16x8_to_f32(ld16(d + c * 8), dv[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(dv[i][e], dv[i][e], ss);
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = rms_inverse(ss, kH);
+    const float lsv = ls ? bf2f(ls[0]) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        const int c = i * kWave + lane;
+        if (c >= NC) continue;
+        float wv[8], rv[8];
+        if (w_post) bf16x8_to_f32(ld16(w_post + c * 8), wv);
+        bf16x8_to_f32(ld16(r + c * 8), rv);
+        uint32_t packed[4];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float n = dv[i][e];
+            if (w_post) n = rbf((n * inv) * wv[e]);
+            float s = rbf(rv[e] + n);
+            if (ls) s = rbf(s * lsv);
+            const uint32_t b = f2bf(s);
+            if (e & 1) packed[e >> 1] |= b << 16; else packed[e >> 1] = b;
+        }
+        *reinterpret_cast<uint4*>(r + c * 8) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+}
+
+// =================================================================== QKV
+// ops::sliding_project_qkv (FO/src/ops.rs:37-76). 8192 projection rows (Q 4096 | K 2048 |
+// V 2048), K = 3840. Four rows per wave, 16 per workgroup, 512 workgroups per token row.
+constexpr int kQkvR = 4;
+constexpr int kQkvRows = kQs + 2 * kPs;
+
+// Per-head epilogue by the head's last wave: RMSNorm over 256 (sliding/rmsnorm.rs:22-153),
+// RoPE on q/k (sliding/rope.rs:9-211), and the q_out / ring-cache stores (ops.rs:72-75).
+// Lane l owns head elements {l, l+64, l+128, l+192}: RoPE partners (e, e+128) share a lane.
+__device__ void qkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict__ raw, int head,
+                                  int m, uint32_t* err) {
+    const int lane = lane_id();
+    const int32_t rope_off = *p.rope_off;
+    const int32_t kv_off = *p.kv_off;
+    const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + m < kE;
+    const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
+    if ((head < 24 && !rope_ok) || (head >= 16 && !kv_ok)) {
+        if (lane == 0) atomicOr(err, rope_ok ? kErrKvOffset : kErrRopeOffset);
+        return;  // nothing is written when an offset is out of range
+    }
+    const int slot = (kv_off / (kNs * kDs * 2) + m) % kTs;
+    float v[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = bf2f(raw[head * kDs + lane + 64 * i]);
+        ss = fmaf(v[i], v[i], ss);
+    }
+    const float inv = rms_inverse(wave_sum(ss), kDs);
+    const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
+    float n[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float y = v[i] * inv;
+        if (wn) y = y * bf2f(wn[lane + 64 * i]);
+        n[i] = rbf(y);
+    }
+    if (head >= 24) {
+        uint16_t* dst = p.v_cache + (size_t)slot * (kNs * kDs) + (head - 24) * kDs;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = (uint16_t)f2bf(n[i]);
+        return;
+    }
+    // y = bf16(bf16(x*cos) + bf16(x_swap*sin_dev)); the table's sin has its low half negated
+    // (generate_references.py:200-210), so x_swap is a plain half swap.
+    const int trow = rope_off / (kDs * 2) + m;
+    const uint16_t* cr = p.cos + (size_t)trow * kDs;
+    const uint16_t* sr = p.sin + (size_t)trow * kDs;
+    uint16_t* dst = head < 16 ? p.q_out + (size_t)m * kQs + head * kDs
+                              : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        const float a = rbf(n[i] * bf2f(cr[e]));
+        const float b = rbf(n[(i + 2) & 3] * bf2f(sr[e]));
+        dst[e] = (uint16_t)f2bf(a + b);
+    }
+}
+
+template <ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0, uint16_t* raw_all,
+                                                            uint32_t* tickets, uint32_t* err) {
+    __shared__ float hs[kH];
+    __shared__ float red[4];
+    constexpr int R = kQkvR, KI = 4;  // 3840 = 3.75 x 1024: lanes >= 48 idle in the last chunk
+    const int m = blockIdx.y;
+    const int lane = lane_id(), wave = wave_id();
+    const int row0 = blockIdx.x * (4 * R) + wave * R;
+    const uint8_t* W;
+    const void* S;
+    int lr;
+    if (row0 < kQs) { W = p.qw; S = p.qs; lr = row0; }
+    else if (row0 < kQs + kPs) { W = p.kw; S = p.ks; lr = row0 - kQs; }
+    else { W = p.vw; S = p.vs; lr = row0 - kQs - kPs; }
+
+    uint4 wq[R][KI];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int col = j * 1024 + lane * 16;
+            wq[r][j] = (col < kH) ? ld_stream(W + (size_t)(lr + r) * kH + col) : make_uint4(0, 0, 0, 0);
+        }
+
+    stage_rmsnorm(p.x + (size_t)(m0 + m) * kH, p.in_rms, hs, red);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        const int col = j * 1024 + lane * 16;
+        if (col < kH) {
+            float h[16];
+            lds_read<16>(hs, col, h);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16(h, wq[r][j], acc[r]);
+        }
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float d = wave_sum(acc[r]);
+        if (lane == r) mine = d;
+    }
+    uint16_t* raw = raw_all + (size_t)m * kQkvRows;
+    if (lane < R) raw[row0 + lane] = (uint16_t)f2bf(mine * load_scale<SK>(S, lr + lane));
+
+    const int head = row0 / kDs;  // 0..15 q, 16..23 k, 24..31 v
+    if (!wave_arrive(&tickets[kTicketQkv + m * 32 + head], kDs / R)) return;
+    qkv_head_epilogue(p, raw, head, m0 + m, err);
+}
+
+// ===================================================================== O
+// ops::sliding_attention_output (FO/src/ops.rs:130-146). 3840 rows, K = 4096. Two rows per
+// wave, 8 per workgroup, 480 workgroups per token row.
+constexpr int kOR = 2;
+
+template <ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uint16_t* pbuf_all,
+                                                          uint32_t* tickets) {
+    __shared__ float xs[kQs];
+    constexpr int R = kOR, KI = kQs / 1024;
+    const int m = blockIdx.y;
+    const int lane = lane_id(), wave = wave_id();
+    const int row0 = blockIdx.x * (4 * R) + wave * R;
+
+    uint4 wq[R][KI];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * kQs + j * 1024 + lane * 16);
+
+    stage_bf16(p.x + (size_t)(m0 + m) * kQs, kQs, xs);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        float h[16];
+        lds_read<16>(xs, j * 1024 + lane * 16, h);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = dot_fp8_16(h, wq[r][j], acc[r]);
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float d = wave_sum(acc[r]);
+        if (lane == r) mine = d;
+    }
+    uint16_t* pbuf = pbuf_all + (size_t)m * kH;
+    if (lane < R) pbuf[row0 + lane] = (uint16_t)f2bf(mine * load_scale<SK>(p.os, row0 + lane));
+
+    if (!wave_arrive(&tickets[kTicketO + m], kH / R)) return;
+    wave_post_residual(pbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, nullptr);
+}
+
+// =================================================================== FFN
+// ops::decoder_feedforward (FO/src/ops.rs:201-239) in two launches:
+//   up_gate: pre-RMSNorm, up and gate rows, GeGLU -> p[15360] (bf16, scratch)
+//   down:    p . W_down rows -> d[3840], then the last wave applies post-norm, residual and
+//            the layer scalar in place.
+constexpr int kUgRL = 8;   // L rows (an up row and a gate row each) per wave
+constexpr int kDownR = 2;  // down rows per wave
+
+template <FfnFormat F>
+constexpr int row_bytes(int k) { return F == FfnFormat::FP8 ? k : k / 2; }
+template <FfnFormat F>
+constexpr int scale_row_bytes(int k) { return F == FfnFormat::NVFP4 ? k / 16 : (F == FfnFormat::MXFP4 ? k / 32 : 0); }
+
+template <FfnFormat F, ScaleKind SK>
+__device__ __forceinline__ float row_scale(const void* s, const float* g, int row) {
+    if constexpr (F == FfnFormat::FP8) return load_scale<SK>(s, row);
+    else if constexpr (F == FfnFormat::NVFP4) return *g;
+    else return 1.0f;
+}
+
+template <FfnFormat F, ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0, uint16_t* pbuf_all) {
+    __shared__ float hs[kH];
+    __shared__ float red[4];
+    constexpr int EPC = elems_per_chunk<F>();
+    constexpr int RB = row_bytes<F>(kH);
+    constexpr int SB = scale_row_bytes<F>(kH);
+    constexpr int KI = (RB + 1023) / 1024;
+    constexpr int RL = kUgRL, G = 1, NG = RL / G;
+    const int m = blockIdx.y;
+    const int lane = lane_id(), wave = wave_id();
+    const int l0 = blockIdx.x * (4 * RL) + wave * RL;
+
+    // Two pipeline stages (A, B) of G L-rows each, in a loop the compiler does not unroll, so
+    // at most two stages of weight chunks are live per wave.
+    Chunk<F> ca[G][2][KI], cbb[G][2][KI];
+    auto issue = [&](int g, Chunk<F> (&dst)[G][2][KI]) {
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int l = l0 + g * G + i;
+#pragma unroll
+            for (int j = 0; j < KI; ++j) {
+                const bool valid = j * 1024 + lane * 16 < RB;
+                load_chunk<F>(dst[i][0][j], p.up + (size_t)l * RB, (const uint8_t*)p.up_s + (size_t)l * SB, j, lane, valid);
+                load_chunk<F>(dst[i][1][j], p.gate + (size_t)l * RB, (const uint8_t*)p.gate_s + (size_t)l * SB, j, lane, valid);
+            }
+        }
+    };
+    issue(0, ca);
+
+    stage_rmsnorm(p.residual + (size_t)(m0 + m) * kH, p.pre_rms, hs, red);
+    float xv[KI][EPC];
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        const int e0 = j * 64 * EPC + lane * EPC;
+        if (e0 < kH) lds_read<EPC>(hs, e0, xv[j]);
+        else {
+#pragma unroll
+            for (int t = 0; t < EPC; ++t) xv[j][t] = 0.0f;
+        }
+    }
+
+    uint16_t* pout = pbuf_all + (size_t)m * kL;
+    auto compute = [&](int g, const Chunk<F> (&src)[G][2][KI]) {
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            float du = 0.0f, dg = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KI; ++j) {
+                du = chunk_dot<F>(xv[j], src[i][0][j], du);
+                dg = chunk_dot<F>(xv[j], src[i][1][j], dg);
+            }
+            du = wave_sum(du);
+            dg = wave_sum(dg);
+            const int l = l0 + g * G + i;
+            const float up = proj_commit<F>(du, row_scale<F, SK>(p.up_s, p.up_g, l));
+            const float gate = proj_commit<F>(dg, row_scale<F, SK>(p.gate_s, p.gate_g, l));
+            // gemma4.py:197: bf16(bf16(gelu_tanh(gate)) * up)
+            if (lane == 0) pout[l] = (uint16_t)f2bf(rbf(gelu_tanh(gate)) * up);
+        }
+    };
+#pragma unroll 1
+    for (int g = 0; g < NG; g += 2) {
+        issue(g + 1, cbb);
+        compute(g, ca);
+        if (g + 2 < NG) issue(g + 2, ca);
+        compute(g + 1, cbb);
+    }
+}
+
+template <FfnFormat F, ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, const uint16_t* pbuf_all,
+                                                          uint16_t* dbuf_all, uint32_t* tickets) {
+    __shared__ float ps[kL];  // 60 KB: two workgroups per CU
+    constexpr int EPC = elems_per_chunk<F>();
+    constexpr int RB = row_bytes<F>(kL);
+    constexpr int SB = scale_row_bytes<F>(kL);
+    constexpr int KI = (RB + 1023) / 1024;
+    constexpr int R = kDownR;
+    const int m = blockIdx.y;
+    const int lane = lane_id(), wave = wave_id();
+    const int row0 = blockIdx.x * (4 * R) + wave * R;
+
+    Chunk<F> cb[R][KI];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < KI; ++j)
+            load_chunk<F>(cb[r][j], p.down + (size_t)(row0 + r) * RB,
+                          p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
+                          j * 1024 + lane * 16 < RB);
+
+    stage_bf16(pbuf_all + (size_t)m * kL, kL, ps);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        const int e0 = j * 64 * EPC + lane * EPC;
+        if (e0 < kL) {
+            float x[EPC];
+            lds_read<EPC>(ps, e0, x);
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = chunk_dot<F>(x, cb[r][j], acc[r]);
+        }
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float d = wave_sum(acc[r]);
+        if (lane == r) mine = d;
+    }
+    uint16_t* dbuf = dbuf_all + (size_t)m * kH;
+    if (lane < R) dbuf[row0 + lane] = (uint16_t)f2bf(proj_commit<F>(mine, row_scale<F, SK>(p.down_s, p.down_g, row0 + lane)));
+
+    if (!wave_arrive(&tickets[kTicketFfn + m], kH / R)) return;
+    wave_post_residual(dbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, p.layer_scalar);
+}
+
+// ========================================================== raw projection
+// out[m, n] = bf16((x[m] . W[n]) * s[n]) for arbitrary N and K % 16 == 0. One row per wave,
+// activations straight from global memory. Used for the raw-projection known answers.
+template <ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void proj_decode_kernel(ProjParams p) {
+    const int m = blockIdx.y;
+    const int lane = lane_id();
+    const int n = blockIdx.x * 4 + wave_id();
+    if (n >= p.N) return;
+    const uint16_t* x = p.x + (size_t)m * p.K;
+    const uint8_t* w = p.w + (size_t)n * p.K;
+    float acc = 0.0f;
+    for (int c = lane * 16; c < p.K; c += 1024) {
+        float h[16];
+        bf16x8_to_f32(ld16(x + c), h);
+        bf16x8_to_f32(ld16(x + c + 8), h + 8);
+        acc = dot_fp8_16(h, ld_stream(w + c), acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) p.out[(size_t)m * p.N + n] = (uint16_t)f2bf(acc * load_scale<SK>(p.s, n));
+}
+
+// ================================================================ self-test
+// Decodes every FP8 code, every FP4 byte (two nibbles, scale 1), every E8M0 code, and GeLU of
+// every bf16 value, with the same device helpers the kernels use.
+//   out[0,256)        f32 bits of E4M3 code i
+//   out[256,768)      f32 bits of the two E2M1 nibbles of byte i (low nibble first)
+//   out[768,1024)     f32 bits of E8M0 code i
+//   out[1024,66560)   bf16 bits of bf16(gelu_tanh(bf16 value i))
+__global__ void format_selftest_kernel(uint32_t* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 256) {
+        float v[4];
+        fp8x4_to_f32((uint32_t)i, v);
+        out[i] = __float_as_uint(v[0]);
+        float w[8];
+        fp4x8_to_f32((uint32_t)i, 1.0f, w);
+        out[256 + 2 * i] = __float_as_uint(w[0]);
+        out[256 + 2 * i + 1] = __float_as_uint(w[1]);
+        out[768 + i] = __float_as_uint(e8m0_to_f32((uint32_t)i));
+    }
+    if (i < 65536) out[1024 + i] = f2bf(gelu_tanh(bf2f((uint32_t)i)));
+}
+
+template <typename K, typename... A>
+hipError_t launch(K kernel, dim3 grid, hipStream_t s, A... args) {
+    hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, s, args...);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
+        const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        const dim3 grid(kQkvRows / (4 * kQkvR), mm);
+        hipError_t e = p.scale_kind == ScaleKind::F32
+            ? launch(qkv_decode_kernel<ScaleKind::F32>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err)
+            : launch(qkv_decode_kernel<ScaleKind::BF16>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
+        const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        const dim3 grid(kH / (4 * kOR), mm);
+        hipError_t e = p.scale_kind == ScaleKind::F32
+            ? launch(o_decode_kernel<ScaleKind::F32>, grid, s, p, m0, ctx->pbuf, ctx->tickets)
+            : launch(o_decode_kernel<ScaleKind::BF16>, grid, s, p, m0, ctx->pbuf, ctx->tickets);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+template <FfnFormat F, ScaleKind SK>
+static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
+        const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        hipError_t e = launch(ffn_up_gate_kernel<F, SK>, dim3(kL / (4 * kUgRL), mm), s, p, m0, ctx->pbuf);
+        if (e != hipSuccess) return e;
+        e = launch(ffn_down_kernel<F, SK>, dim3(kH / (4 * kDownR), mm), s, p, m0,
+                   (const uint16_t*)ctx->pbuf, ctx->dbuf, ctx->tickets);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_ffn_decode(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    switch (p.fmt) {
+        case FfnFormat::FP8:
+            return p.scale_kind == ScaleKind::F32 ? ffn_decode_impl<FfnFormat::FP8, ScaleKind::F32>(p, M, s, ctx)
+                                                  : ffn_decode_impl<FfnFormat::FP8, ScaleKind::BF16>(p, M, s, ctx);
+        case FfnFormat::NVFP4: return ffn_decode_impl<FfnFormat::NVFP4, ScaleKind::F32>(p, M, s, ctx);
+        case FfnFormat::MXFP4: return ffn_decode_impl<FfnFormat::MXFP4, ScaleKind::F32>(p, M, s, ctx);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s) {
+    const dim3 grid((p.N + 3) / 4, M);
+    return p.scale_kind == ScaleKind::F32 ? launch(proj_decode_kernel<ScaleKind::F32>, grid, s, p)
+                                          : launch(proj_decode_kernel<ScaleKind::BF16>, grid, s, p);
+}
+
+hipError_t launch_format_selftest(uint32_t* out, hipStream_t s) {
+    return launch(format_selftest_kernel, dim3(65536 / kBlock), s, out);
+}
+
+}  // namespace moa

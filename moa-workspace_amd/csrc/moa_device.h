@@ -1,0 +1,104 @@
+// moa_device.h -- device-side helpers shared by the gfx950 kernels.
+//
+// Number formats follow the reference's oracle exactly:
+//   bf16 <-> f32 is round-half-to-even on the raw bits (FO/scripts/fixture_prng.py:80-90);
+//   E4M3FN codes widen exactly (FO/scripts/generate_references.py:152);
+//   E2M1 nibbles are low-nibble-first, magnitude {0,.5,1,1.5,2,3,4,6} (generate_references.py:69,154-163).
+// The file is compiled with -ffp-contract=off: every multiply and add rounds on its own
+// unless a kernel calls fmaf() where the product is exact (bf16 x fp8/fp4 products are).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moa_shapes.h"
+
+namespace moa {
+
+constexpr int kWave = 64;
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float v) {
+    uint32_t b = __float_as_uint(v);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+}
+
+// Round an f32 through bf16 and back (the per-op bf16 commit of a torch bf16 tensor op).
+__device__ __forceinline__ float rbf(float v) { return bf2f(f2bf(v)); }
+
+// Eight packed bf16 (one 16-byte load) to f32.
+__device__ __forceinline__ void bf16x8_to_f32(const uint4& q, float* o) {
+    o[0] = __uint_as_float(q.x << 16); o[1] = __uint_as_float(q.x & 0xffff0000u);
+    o[2] = __uint_as_float(q.y << 16); o[3] = __uint_as_float(q.y & 0xffff0000u);
+    o[4] = __uint_as_float(q.z << 16); o[5] = __uint_as_float(q.z & 0xffff0000u);
+    o[6] = __uint_as_float(q.w << 16); o[7] = __uint_as_float(q.w & 0xffff0000u);
+}
+
+// ---------------------------------------------------------- fp8 / fp4 decode
+// gfx950 converts OCP E4M3FN in hardware; two codes per instruction.
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* o) {
+    f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+    f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+    o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
+}
+
+// Eight E2M1 nibbles of one dword (low nibble = lower element index), each times `scale`.
+// The product e2m1 * scale is exact in f32 for E4M3 and power-of-two scales.
+__device__ __forceinline__ void fp4x8_to_f32(uint32_t w, float scale, float* o) {
+    f32x2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
+    f32x2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);
+    f32x2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 2);
+    f32x2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 3);
+    o[0] = a[0]; o[1] = a[1]; o[2] = b[0]; o[3] = b[1];
+    o[4] = c[0]; o[5] = c[1]; o[6] = d[0]; o[7] = d[1];
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t code) {
+    return __builtin_amdgcn_cvt_pk_f32_fp8(code & 0xffu, false)[0];
+}
+
+// E8M0 exponent -> 2^(e-127) as f32 (0xff is NaN in OCP MX; callers never pass it).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+    e &= 0xffu;
+    return e == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23);
+}
+
+// ------------------------------------------------------------- reductions
+// xor butterfly: every lane ends with the same bits (f32 add is commutative).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// ----------------------------------------------------------------- loads
+// Weights are read exactly once per call: stream them non-temporally.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// torch.rsqrt on CPU is 1/sqrt with both steps correctly rounded (gemma4.py:86).
+__device__ __forceinline__ float rms_inverse(float sum_sq, int n) {
+    float mean = __fdiv_rn(sum_sq, (float)n);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, kEps)));
+}
+
+// torch gelu(approximate="tanh") in f32 (gemma4.py:197): 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float kBeta = 0.7978845608028654f;
+    const float kKappa = 0.044715f;
+    float cube = x * x * x;
+    float inner = kBeta * (x + kKappa * cube);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+}  // namespace moa

@@ -1,0 +1,84 @@
+// moa_internal.h -- host-side declarations shared by the C-ABI and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moa_shapes.h"
+
+namespace moa {
+
+// Rows handled by the decode (GEMV) kernels in one launch; larger M goes to the MFMA path.
+constexpr int kMaxDecodeM = 16;
+// Rows handled by one call of the MFMA (M > kMaxDecodeM) path; larger calls are tiled by the host.
+constexpr int kMaxChunkM = 1024;
+
+// Ticket slots: [0, 32*kMaxDecodeM) QKV heads; then O; then FFN down.
+constexpr int kTicketQkv = 0;
+constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
+constexpr int kTicketFfn = kTicketO + kMaxDecodeM;
+constexpr int kTicketCount = kTicketFfn + kMaxDecodeM;
+
+// Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
+constexpr uint32_t kErrRopeOffset = 1u;
+constexpr uint32_t kErrKvOffset = 2u;
+constexpr uint32_t kErrSpinTimeout = 4u;
+
+// Per-device persistent scratch, allocated once on first use (never per call).
+struct DevCtx {
+    int device = -1;
+    uint32_t* tickets = nullptr;  // kTicketCount, zero between calls (self-resetting)
+    uint32_t* err = nullptr;      // 4 words
+    uint16_t* raw_qkv = nullptr;  // [kMaxChunkM, 8192] bf16 raw projections
+    uint16_t* pbuf = nullptr;     // [kMaxChunkM, 15360] bf16 (O: [M,3840]; FFN: GeGLU output)
+    uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
+    uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
+    void* base = nullptr;
+};
+
+// Returns the context of the current device, allocating it on first use. nullptr on failure.
+DevCtx* device_context(hipError_t* err);
+
+enum class ScaleKind { F32, BF16 };
+enum class FfnFormat { FP8, NVFP4, MXFP4 };
+
+struct QkvParams {
+    const uint16_t* x; const uint8_t* qw; const uint8_t* kw; const uint8_t* vw;
+    const void* qs; const void* ks; const void* vs; ScaleKind scale_kind;
+    const uint16_t* in_rms; const uint16_t* q_rms; const uint16_t* k_rms;
+    const int32_t* kv_off; const int32_t* rope_off; const uint16_t* cos; const uint16_t* sin;
+    uint16_t* k_cache; uint16_t* v_cache; uint16_t* q_out;
+};
+
+struct OParams {
+    const uint16_t* x; const uint16_t* post_rms; const uint8_t* ow; const void* os; ScaleKind scale_kind;
+    uint16_t* residual;
+};
+
+struct FfnParams {
+    FfnFormat fmt;
+    uint16_t* residual; const uint16_t* pre_rms;
+    const uint8_t* up; const uint8_t* gate; const uint8_t* down;
+    const void* up_s; const void* gate_s; const void* down_s;  // FP8: f32|bf16 per row; FP4: u8 codes
+    ScaleKind scale_kind;                                        // FP8 only
+    const float* up_g; const float* gate_g; const float* down_g; // NVFP4 reciprocal globals (device)
+    const uint16_t* post_rms; const uint16_t* layer_scalar;      // nullable
+};
+
+struct ProjParams {  // raw FP8 projection out[m,n] = bf16((x[m].W[n]) * s[n])
+    const uint16_t* x; const uint8_t* w; const void* s; ScaleKind scale_kind; uint16_t* out;
+    int N, K;
+};
+
+hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_ffn_decode(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s);
+
+hipError_t launch_qkv_chunk(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_o_chunk(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_ffn_chunk(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx);
+
+hipError_t launch_format_selftest(uint32_t* out, hipStream_t s);
+
+}  // namespace moa

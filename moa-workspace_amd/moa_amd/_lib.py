@@ -1,0 +1,77 @@
+"""ctypes binding of libmoa_gfx950.so (declarations mirror include/moa_ops.h).
+
+Loading fails loudly when the library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("MOA_LIB", PKG_ROOT / "libmoa_gfx950.so"))
+
+MOA_SUCCESS = 0
+ERRORS = {
+    -1: "MOA_ERROR_INVALID_VALUE",
+    -2: "MOA_ERROR_MISALIGNED",
+    -3: "MOA_ERROR_HIP",
+    -4: "MOA_ERROR_NO_DEVICE",
+    -5: "MOA_ERROR_DEVICE_STATE",
+}
+DEVERR_ROPE_OFFSET = 1
+DEVERR_KV_OFFSET = 2
+
+
+class MoaError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {message}")
+        self.code = code
+
+
+P, I32, U32P = C.c_void_p, C.c_int, C.POINTER(C.c_uint32)
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+SIGNATURES = {
+    "moa_version": [],
+    "moa_last_error_string": [],
+    "moa_init": [I32],
+    "moa_device_errors": [P, U32P],
+    "moa_sliding_project_qkv": [P] * 17 + [I32, P],
+    "moa_sliding_project_qkv_bf16_scales": [P] * 17 + [I32, P],
+    "moa_sliding_attention_output": [P] * 5 + [I32, P],
+    "moa_sliding_attention_output_bf16_scales": [P] * 5 + [I32, P],
+    "moa_decoder_feedforward": [P] * 13 + [I32, P],
+    "moa_decoder_feedforward_fp8": [P] * 10 + [I32, P],
+    "moa_decoder_feedforward_mxfp4": [P] * 10 + [I32, P],
+    "moa_fp8_scaled_projection": [P] * 4 + [I32, I32, I32, P],
+    "moa_format_selftest": [P, P],
+}
+_RESTYPES = {"moa_version": C.c_char_p, "moa_last_error_string": C.c_char_p}
+
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Load and declare the library (once). Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise MoaError(-4, f"{LIB_PATH} is not built; run `python moa-workspace_amd/build.py`")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, C.c_int)
+    _lib = lib
+    return lib
+
+
+def check(code: int) -> None:
+    if code != MOA_SUCCESS:
+        raise MoaError(code, load().moa_last_error_string().decode())
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

@@ -1,0 +1,175 @@
+"""The reference operator interface (FO/src/ops.rs) over the gfx950 C ABI.
+
+Each function keeps the argument order and in-place semantics of the reference's
+`#[device] fn` (the `device` handle becomes torch device memory on the current HIP
+stream). Tensors are torch tensors on a ROCm device:
+
+  bf16 tensors    torch.bfloat16 (or int16/uint16 bit views)
+  E4M3 / E2M1 / E8M0 codes    torch.uint8 (E4M3 may also be torch.float8_e4m3fn)
+  per-channel scales    torch.float32 (ops.rs uses bf16: pass torch.bfloat16 and the
+                        exact bf16 entry point is used)
+
+Errors from the library raise MoaError; nothing falls back to a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+
+H, L, NS, GS, DS, QS, PS, TS, E = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768
+
+
+def _ptr(t: torch.Tensor | None, name: str, dtypes, numel: int | None = None):
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on a ROCm device, got {t.device}")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name}: expected {numel} elements, got {t.numel()}")
+    return C.c_void_p(t.data_ptr())
+
+
+_BF16 = (torch.bfloat16, torch.int16, torch.uint16)
+_U8 = (torch.uint8, torch.float8_e4m3fn)
+_F32 = (torch.float32,)
+_I32 = (torch.int32,)
+
+
+def _stream(t: torch.Tensor) -> C.c_void_p:
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _rows(x: torch.Tensor, width: int, name: str) -> int:
+    if x.numel() % width:
+        raise ValueError(f"{name}: {x.numel()} elements is not a multiple of {width}")
+    return x.numel() // width
+
+
+def _scales(*ts):
+    kinds = {t.dtype for t in ts}
+    if kinds == {torch.float32}:
+        return _F32, False
+    if kinds <= set(_BF16):
+        return _BF16, True
+    raise TypeError(f"per-channel scales must all be float32 or all bfloat16, got {kinds}")
+
+
+def sliding_project_qkv(x, q_weight, k_weight, v_weight, q_weight_scale, k_weight_scale, v_weight_scale,
+                        input_rms_weight, q_rms_weight, k_rms_weight, kv_offset, rope_offset, cos, sin,
+                        k_cache, v_cache, q_out) -> None:
+    """ops::sliding_project_qkv (FO/src/ops.rs:37-76). Writes q_out and the K/V cache slot(s)."""
+    M = _rows(x, H, "x")
+    sd, bf = _scales(q_weight_scale, k_weight_scale, v_weight_scale)
+    args = [
+        _ptr(x, "x", _BF16), _ptr(q_weight, "q_weight", _U8, QS * H), _ptr(k_weight, "k_weight", _U8, PS * H),
+        _ptr(v_weight, "v_weight", _U8, PS * H), _ptr(q_weight_scale, "q_weight_scale", sd, QS),
+        _ptr(k_weight_scale, "k_weight_scale", sd, PS), _ptr(v_weight_scale, "v_weight_scale", sd, PS),
+        _ptr(input_rms_weight, "input_rms_weight", _BF16, H), _ptr(q_rms_weight, "q_rms_weight", _BF16, DS),
+        _ptr(k_rms_weight, "k_rms_weight", _BF16, DS), _ptr(kv_offset, "kv_offset", _I32, 1),
+        _ptr(rope_offset, "rope_offset", _I32, 1), _ptr(cos, "cos", _BF16, E * DS), _ptr(sin, "sin", _BF16, E * DS),
+        _ptr(k_cache, "k_cache", _BF16, TS * NS * DS), _ptr(v_cache, "v_cache", _BF16, TS * NS * DS),
+        _ptr(q_out, "q_out", _BF16, M * QS),
+    ]
+    name = "moa_sliding_project_qkv_bf16_scales" if bf else "moa_sliding_project_qkv"
+    _lib.call(name, *args, M, _stream(x))
+
+
+def sliding_attention_output(x, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
+    """ops::sliding_attention_output (FO/src/ops.rs:130-146). Updates residual in place."""
+    M = _rows(x, QS, "x")
+    sd, bf = _scales(o_weight_scale)
+    args = [
+        _ptr(x, "x", _BF16), _ptr(post_attn_rms_weight, "post_attn_rms_weight", _BF16, H),
+        _ptr(o_weight, "o_weight", _U8, H * QS), _ptr(o_weight_scale, "o_weight_scale", sd, H),
+        _ptr(residual, "residual", _BF16, M * H),
+    ]
+    name = "moa_sliding_attention_output_bf16_scales" if bf else "moa_sliding_attention_output"
+    _lib.call(name, *args, M, _stream(x))
+
+
+def decoder_feedforward(residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed, down_weight_packed,
+                        up_weight_scale, gate_weight_scale, down_weight_scale, up_global_scale, gate_global_scale,
+                        down_global_scale, post_ff_rms_weight, layer_scalar) -> None:
+    """ops::decoder_feedforward (FO/src/ops.rs:201-239), NVFP4 weights. Updates residual in place."""
+    M = _rows(residual, H, "residual")
+    args = [
+        _ptr(residual, "residual", _BF16), _ptr(pre_ff_rms_weight, "pre_ff_rms_weight", _BF16, H),
+        _ptr(up_weight_packed, "up_weight_packed", _U8, L * H // 2),
+        _ptr(gate_weight_packed, "gate_weight_packed", _U8, L * H // 2),
+        _ptr(down_weight_packed, "down_weight_packed", _U8, H * L // 2),
+        _ptr(up_weight_scale, "up_weight_scale", _U8, L * H // 16),
+        _ptr(gate_weight_scale, "gate_weight_scale", _U8, L * H // 16),
+        _ptr(down_weight_scale, "down_weight_scale", _U8, H * L // 16),
+        _ptr(up_global_scale, "up_global_scale", _F32, 1), _ptr(gate_global_scale, "gate_global_scale", _F32, 1),
+        _ptr(down_global_scale, "down_global_scale", _F32, 1),
+        _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
+    ]
+    _lib.call("moa_decoder_feedforward", *args, M, _stream(residual))
+
+
+def decoder_feedforward_fp8(residual, pre_ff_rms_weight, up_weight, gate_weight, down_weight, up_weight_scale,
+                            gate_weight_scale, down_weight_scale, post_ff_rms_weight=None, layer_scalar=None) -> None:
+    """GeGLU FFN with FP8 E4M3 weights and f32 per-channel scales."""
+    M = _rows(residual, H, "residual")
+    args = [
+        _ptr(residual, "residual", _BF16), _ptr(pre_ff_rms_weight, "pre_ff_rms_weight", _BF16, H),
+        _ptr(up_weight, "up_weight", _U8, L * H), _ptr(gate_weight, "gate_weight", _U8, L * H),
+        _ptr(down_weight, "down_weight", _U8, H * L), _ptr(up_weight_scale, "up_weight_scale", _F32, L),
+        _ptr(gate_weight_scale, "gate_weight_scale", _F32, L), _ptr(down_weight_scale, "down_weight_scale", _F32, H),
+        _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
+    ]
+    _lib.call("moa_decoder_feedforward_fp8", *args, M, _stream(residual))
+
+
+def decoder_feedforward_mxfp4(residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed, down_weight_packed,
+                              up_weight_scale, gate_weight_scale, down_weight_scale, post_ff_rms_weight=None,
+                              layer_scalar=None) -> None:
+    """GeGLU FFN with MXFP4 weights (E2M1 + E8M0 per 32)."""
+    M = _rows(residual, H, "residual")
+    args = [
+        _ptr(residual, "residual", _BF16), _ptr(pre_ff_rms_weight, "pre_ff_rms_weight", _BF16, H),
+        _ptr(up_weight_packed, "up_weight_packed", _U8, L * H // 2),
+        _ptr(gate_weight_packed, "gate_weight_packed", _U8, L * H // 2),
+        _ptr(down_weight_packed, "down_weight_packed", _U8, H * L // 2),
+        _ptr(up_weight_scale, "up_weight_scale", _U8, L * H // 32),
+        _ptr(gate_weight_scale, "gate_weight_scale", _U8, L * H // 32),
+        _ptr(down_weight_scale, "down_weight_scale", _U8, H * L // 32),
+        _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
+    ]
+    _lib.call("moa_decoder_feedforward_mxfp4", *args, M, _stream(residual))
+
+
+def fp8_scaled_projection(x, w, scale, out) -> None:
+    """scaled_projection (FO/scripts/generate_references.py:265-274): out = bf16((x . W^T) * scale)."""
+    N, K = w.shape
+    M = _rows(x, K, "x")
+    args = [_ptr(x, "x", _BF16), _ptr(w, "w", _U8, N * K), _ptr(scale, "scale", _F32, N),
+            _ptr(out, "out", _BF16, M * N)]
+    _lib.call("moa_fp8_scaled_projection", *args, M, N, K, _stream(x))
+
+
+def device_errors(device: torch.device | None = None) -> int:
+    """Synchronise the current stream; return and clear the kernel-raised error bits."""
+    bits = C.c_uint32(0)
+    s = torch.cuda.current_stream(device).cuda_stream
+    _lib.call("moa_device_errors", C.c_void_p(s), C.byref(bits))
+    return int(bits.value)
+
+
+def format_selftest(device="cuda") -> torch.Tensor:
+    out = torch.zeros(66560, dtype=torch.int32, device=device)  # layout: moa_decode.hip format_selftest_kernel
+    _lib.call("moa_format_selftest", C.c_void_p(out.data_ptr()), _stream(out))
+    return out
+
+
+def init(device: int = 0) -> None:
+    _lib.call("moa_init", device)

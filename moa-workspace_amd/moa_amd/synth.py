@@ -1,0 +1,225 @@
+"""Inputs for the three operators (host numpy arrays; bf16 as uint16 bits).
+
+Two families:
+  * reference runs -- the exact inputs of the reference harness's run `r`, seeded
+    `run{r}.{test}.{tensor}` (FO/src/bin/test_kernels.rs:481-624, generate_references.py:291-414);
+  * BASELINE configs -- the measurement workloads (normal weights quantised to FP8 per channel
+    or MXFP4, N(0,1) activations), drawn from a generator keyed by
+    `cfg{k}.seed{s}.{tensor}` (numpy PCG64 seeded by the name's FNV-1a hash).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import formats as F
+from . import prng
+
+H, L, NS, GS, DS, QS, PS, TS, E = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768
+
+# Reference distributions (test_kernels.rs:147-155; generate_references.py:64-77).
+WEIGHT_EXP = (7, 14)
+LOCAL_SCALE_EXP = (8, 10)
+ROW_SCALE = (0.0, 1e-3)
+UNIT = (0.0, 1.0)
+RMS_WEIGHT = (0.75, 1.25)
+ACTIVATION = (-1.0, 1.0)
+GLOBAL_SCALE = (2048.0, 16384.0)
+LAYER_SCALAR = 0.375
+
+
+def rope_row(head_dim: int, theta: float, factor: float, pos: int):
+    """cos, sin for one position in f64, narrowed to f32 (generate_references.py:184-197)."""
+    angles = int(factor * head_dim // 2)
+    inv = 1.0 / (np.float64(theta) ** (np.arange(0, 2 * angles, 2, dtype=np.float64) / head_dim))
+    inv = np.concatenate([inv, np.zeros(head_dim // 2 - angles)])
+    emb = np.concatenate([pos * inv, pos * inv])
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+
+
+def kernel_sin(sin: np.ndarray) -> np.ndarray:
+    """The sin operand the kernel receives: low half negated (generate_references.py:200-210)."""
+    out = sin.copy()
+    out[: out.size // 2] *= -1.0
+    return out
+
+
+def rope_tables(positions, theta: float = 10_000.0):
+    """Full [E, 256] bf16 cos/sin tables with the given rows filled (zeros elsewhere, as the
+    reference harness builds them, test_kernels.rs:421-439)."""
+    cos = np.zeros((E, DS), np.uint16)
+    sin = np.zeros((E, DS), np.uint16)
+    for p in positions:
+        c, s = rope_row(DS, theta, 1.0, int(p))
+        cos[p] = prng.f32_to_bf16_bits(c)
+        sin[p] = prng.f32_to_bf16_bits(kernel_sin(s))
+    return cos, sin
+
+
+# ----------------------------------------------------------- reference runs
+
+class RefSynth:
+    """One (run, test) pair of the reference harness; records each input's checksum."""
+
+    def __init__(self, test: str, run: int):
+        self.test, self.run = test, run
+        self.checks: dict[str, int] = {}
+
+    def seed(self, name: str) -> str:
+        return f"run{self.run}.{self.test}.{name}"
+
+    def keep(self, name: str, a: np.ndarray) -> np.ndarray:
+        self.checks[name] = prng.checksum(a)
+        return a
+
+    def bf16(self, name, count, span):
+        return self.keep(name, prng.bf16_uniform(self.seed(name), count, *span))
+
+    def f8(self, name, count, band, signed=True):
+        return self.keep(name, prng.f8_banded(self.seed(name), count, band[0], band[1], signed))
+
+    def f4(self, name, count):
+        return self.keep(name, prng.f4_nibbles(self.seed(name), count))
+
+
+def ref_qkv_inputs(run: int) -> dict:
+    """test_kernels.rs:481-546 / generate_references.py:291-334."""
+    s = RefSynth("sliding_project_qkv", run)
+    pos = prng.run_pos(run)
+    in_rms = s.bf16("input_rms_weight", H, RMS_WEIGHT)
+    signs = s.keep("x_signs", prng.bf16_signs(s.seed("x_signs"), H, 1.0))
+    # x = bf16(sign / input_rms_weight): normalises to one magnitude with the drawn signs (test_kernels.rs:360-379)
+    x = s.keep("x_exact", prng.f32_to_bf16_bits(prng.bf16_bits_to_f32(signs) / prng.bf16_bits_to_f32(in_rms)))
+    d = dict(
+        x=x, input_rms_weight=in_rms,
+        q_weight=s.f8("q_weight", QS * H, WEIGHT_EXP).reshape(QS, H),
+        k_weight=s.f8("k_weight", PS * H, WEIGHT_EXP).reshape(PS, H),
+        v_weight=s.f8("v_weight", PS * H, WEIGHT_EXP).reshape(PS, H),
+        q_weight_scale=s.bf16("q_weight_scale", QS, ROW_SCALE),
+        k_weight_scale=s.bf16("k_weight_scale", PS, ROW_SCALE),
+        v_weight_scale=s.bf16("v_weight_scale", PS, ROW_SCALE),
+        q_rms_weight=s.bf16("q_rms_weight", DS, UNIT),
+        k_rms_weight=s.bf16("k_rms_weight", DS, UNIT),
+        pos=pos,
+    )
+    d["cos"], d["sin"] = rope_tables([pos])
+    s.keep("cos", d["cos"][pos])
+    s.keep("sin", d["sin"][pos])
+    d["rope_offset"] = pos * DS * 2
+    d["kv_offset"] = (pos % TS) * NS * DS * 2
+    d["checks"] = s.checks
+    return d
+
+
+def ref_o_inputs(run: int) -> dict:
+    """test_kernels.rs:548-570 / generate_references.py:337-355."""
+    s = RefSynth("sliding_attention_output", run)
+    d = dict(
+        x=s.bf16("x", QS, ACTIVATION),
+        post_attn_rms_weight=s.bf16("post_attn_rms_weight", H, UNIT),
+        o_weight=s.f8("o_weight", H * QS, WEIGHT_EXP).reshape(H, QS),
+        o_weight_scale=s.bf16("o_weight_scale", H, ROW_SCALE),
+        residual=s.bf16("residual", H, UNIT),
+    )
+    d["checks"] = s.checks
+    return d
+
+
+def ref_ffn_inputs(run: int) -> dict:
+    """test_kernels.rs:572-624 / generate_references.py:375-414 (NVFP4)."""
+    s = RefSynth("decoder_feedforward", run)
+    d = dict(
+        residual=s.bf16("residual", H, UNIT),
+        pre_ff_rms_weight=s.bf16("pre_ff_rms_weight", H, UNIT),
+        post_ff_rms_weight=s.bf16("post_ff_rms_weight", H, UNIT),
+    )
+    for name, rows, cols in (("up", L, H), ("gate", L, H), ("down", H, L)):
+        d[f"{name}_weight_packed"] = s.f4(f"{name}_weight_packed", rows * cols).reshape(rows, cols // 2)
+        d[f"{name}_weight_scale"] = s.f8(f"{name}_weight_scale", rows * cols // 16, LOCAL_SCALE_EXP, False).reshape(rows, cols // 16)
+        g = prng.f32_uniform(f"run{run}.global.{name}_global_scale", 1, *GLOBAL_SCALE)[0]
+        d[f"{name}_global_scale"] = np.array([np.float32(1.0) / g], np.float32)
+        s.keep(f"{name}_global_scale", d[f"{name}_global_scale"])
+    d["layer_scalar"] = s.keep("layer_scalar", prng.f32_to_bf16_bits(np.full(8, LAYER_SCALAR, np.float32)))
+    d["checks"] = s.checks
+    return d
+
+
+# --------------------------------------------------------- BASELINE configs
+
+def _gen(name: str) -> np.random.Generator:
+    """numpy PCG64 generator seeded by the FNV-1a hash of the tensor's name."""
+    return np.random.Generator(np.random.PCG64(prng.name_hash(name)))
+
+
+def normal(name: str, shape, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    z = _gen(name).standard_normal(size=shape, dtype=np.float32)
+    return (z * np.float32(std) + np.float32(mean)).astype(np.float32)
+
+
+def bf16_normal(name: str, shape, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    return prng.f32_to_bf16_bits(normal(name, shape, std, mean))
+
+
+def rms_weight(name: str, n: int) -> np.ndarray:
+    """RMSNorm weight stored as the value 1 + w, w ~ N(0, 0.1)."""
+    return prng.f32_to_bf16_bits(np.float32(1.0) + normal(name, (n,), 0.1))
+
+
+def fp8_weight(name: str, rows: int, cols: int):
+    return F.quantize_fp8_rows(normal(name, (rows, cols), 0.02))
+
+
+def mxfp4_weight(name: str, rows: int, cols: int):
+    return F.quantize_mxfp4(normal(name, (rows, cols), 0.02))
+
+
+def cfg_ffn_fp8(seed: int = 0, M: int = 1, tag: str = "cfg0") -> dict:
+    """Config 0: FP8 E4M3 per-channel FFN; post-norm weight and layer scalar included (the
+    full FO/src/ops.rs:201-239 contract)."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    up, su = fp8_weight(n("up"), L, H)
+    gate, sg = fp8_weight(n("gate"), L, H)
+    down, sd = fp8_weight(n("down"), H, L)
+    return dict(residual=bf16_normal(n("residual"), (M, H)), pre_ff_rms_weight=rms_weight(n("pre_rms"), H),
+                post_ff_rms_weight=rms_weight(n("post_rms"), H),
+                layer_scalar=prng.f32_to_bf16_bits(np.full(8, LAYER_SCALAR, np.float32)),
+                up_weight=up, gate_weight=gate, down_weight=down,
+                up_weight_scale=su, gate_weight_scale=sg, down_weight_scale=sd)
+
+
+def cfg_o(seed: int = 0, M: int = 1, tag: str = "cfg1") -> dict:
+    """Config 1: attention-output projection, FP8 W_o [3840,4096] per-channel f32 scales."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    ow, os_ = fp8_weight(n("o"), H, QS)
+    return dict(x=bf16_normal(n("x"), (M, QS)), post_attn_rms_weight=rms_weight(n("post_rms"), H),
+                o_weight=ow, o_weight_scale=os_, residual=bf16_normal(n("residual"), (M, H)))
+
+
+def cfg_qkv(seed: int = 0, M: int = 1, tag: str = "cfg2", theta: float = 10_000.0, pos: int | None = None) -> dict:
+    """Config 2: fused QKV at a random position p in [0, 8191] (rows p..p+M-1), ring slot p mod 1024,
+    every other cache slot pre-filled N(0,1)."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    if pos is None:
+        pos = int(prng.words(n("pos"), 1)[0] % np.uint64(8192))
+    qw, qs = fp8_weight(n("q"), QS, H)
+    kw, ks = fp8_weight(n("k"), PS, H)
+    vw, vs = fp8_weight(n("v"), PS, H)
+    cos, sin = rope_tables(range(pos, pos + M), theta)
+    return dict(x=bf16_normal(n("x"), (M, H)), q_weight=qw, k_weight=kw, v_weight=vw,
+                q_weight_scale=qs, k_weight_scale=ks, v_weight_scale=vs,
+                input_rms_weight=rms_weight(n("in_rms"), H), q_rms_weight=rms_weight(n("q_rms"), DS),
+                k_rms_weight=rms_weight(n("k_rms"), DS), pos=pos,
+                rope_offset=pos * DS * 2, kv_offset=(pos % TS) * NS * DS * 2, cos=cos, sin=sin,
+                k_cache=bf16_normal(n("k_cache"), (TS, NS, DS)), v_cache=bf16_normal(n("v_cache"), (TS, NS, DS)))
+
+
+def cfg_ffn_mxfp4(seed: int = 0, M: int = 1, tag: str = "cfg3") -> dict:
+    """Config 3: MXFP4 FFN (E2M1 + E8M0 per 32 along K)."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    up, su = mxfp4_weight(n("up"), L, H)
+    gate, sg = mxfp4_weight(n("gate"), L, H)
+    down, sd = mxfp4_weight(n("down"), H, L)
+    return dict(residual=bf16_normal(n("residual"), (M, H)), pre_ff_rms_weight=rms_weight(n("pre_rms"), H),
+                post_ff_rms_weight=rms_weight(n("post_rms"), H),
+                layer_scalar=prng.f32_to_bf16_bits(np.full(8, LAYER_SCALAR, np.float32)),
+                up_weight_packed=up, gate_weight_packed=gate, down_weight_packed=down,
+                up_weight_scale=su, gate_weight_scale=sg, down_weight_scale=sd)

@@ -1,0 +1,148 @@
+"""ops::decoder_feedforward (NVFP4, as the reference), and the FP8 / MXFP4 weight variants,
+on the GPU vs the CPU oracle and the reference's known answer."""
+import numpy as np
+import pytest
+
+from gpu_util import dev, gate, host, need_gpu, say, torch
+from kat_inputs import GOLDEN, ffn_stress_inputs, unbf
+from moa_amd import prng, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FFN_ATOL = 1e-2  # the reference's own FFN atol (test_kernels.rs:461-464) equals BASELINE's
+
+
+def gpu_nvfp4(d):
+    from moa_amd import ops
+    r = dev(d["residual"])
+    ops.decoder_feedforward(r, dev(d["pre_ff_rms_weight"]), dev(d["up_weight_packed"]), dev(d["gate_weight_packed"]),
+                            dev(d["down_weight_packed"]), dev(d["up_weight_scale"]), dev(d["gate_weight_scale"]),
+                            dev(d["down_weight_scale"]), dev(d["up_global_scale"]), dev(d["gate_global_scale"]),
+                            dev(d["down_global_scale"]), dev(d["post_ff_rms_weight"]), dev(d["layer_scalar"]))
+    return host(r)
+
+
+def oracle_nvfp4(d):
+    w = O.ffn_weights(O.FFN_NVFP4, d["up_weight_packed"], d["gate_weight_packed"], d["down_weight_packed"],
+                      d["up_weight_scale"], d["gate_weight_scale"], d["down_weight_scale"],
+                      (d["up_global_scale"][0], d["gate_global_scale"][0], d["down_global_scale"][0]))
+    r = d["residual"].copy()
+    O.decoder_feedforward(r, d["pre_ff_rms_weight"], w, d["post_ff_rms_weight"], d["layer_scalar"])
+    return r
+
+
+def gpu_fp8(d, post=True, ls=True):
+    from moa_amd import ops
+    r = dev(d["residual"])
+    ops.decoder_feedforward_fp8(r, dev(d["pre_ff_rms_weight"]), dev(d["up_weight"]), dev(d["gate_weight"]),
+                                dev(d["down_weight"]), dev(d["up_weight_scale"]), dev(d["gate_weight_scale"]),
+                                dev(d["down_weight_scale"]), dev(d["post_ff_rms_weight"]) if post else None,
+                                dev(d["layer_scalar"]) if ls else None)
+    return host(r)
+
+
+def oracle_fp8(d, post=True, ls=True):
+    w = O.ffn_weights(O.FFN_FP8, d["up_weight"], d["gate_weight"], d["down_weight"], d["up_weight_scale"],
+                      d["gate_weight_scale"], d["down_weight_scale"])
+    r = d["residual"].copy()
+    O.decoder_feedforward(r, d["pre_ff_rms_weight"], w, d["post_ff_rms_weight"] if post else None,
+                          d["layer_scalar"] if ls else None)
+    return r
+
+
+def gpu_mxfp4(d):
+    from moa_amd import ops
+    r = dev(d["residual"])
+    ops.decoder_feedforward_mxfp4(r, dev(d["pre_ff_rms_weight"]), dev(d["up_weight_packed"]),
+                                  dev(d["gate_weight_packed"]), dev(d["down_weight_packed"]),
+                                  dev(d["up_weight_scale"]), dev(d["gate_weight_scale"]),
+                                  dev(d["down_weight_scale"]), dev(d["post_ff_rms_weight"]), dev(d["layer_scalar"]))
+    return host(r)
+
+
+def oracle_mxfp4(d):
+    w = O.ffn_weights(O.FFN_MXFP4, d["up_weight_packed"], d["gate_weight_packed"], d["down_weight_packed"],
+                      d["up_weight_scale"], d["gate_weight_scale"], d["down_weight_scale"])
+    r = d["residual"].copy()
+    O.decoder_feedforward(r, d["pre_ff_rms_weight"], w, d["post_ff_rms_weight"], d["layer_scalar"])
+    return r
+
+
+def test_nvfp4_stress_known_answer():
+    """full-ffn-stress: 3840 x 0x3ecf through the reference-contract NVFP4 entry point."""
+    need_gpu()
+    say("ffn nvfp4 stress")
+    got = gpu_nvfp4(ffn_stress_inputs())
+    want = np.fromfile(GOLDEN / "ffn_stress_expected_bf16.bin", dtype="<u2")
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("run", range(3))
+def test_nvfp4_reference_runs(run):
+    need_gpu()
+    say(f"ffn nvfp4 reference run {run}")
+    d = synth.ref_ffn_inputs(run)
+    gate(oracle_nvfp4(d), gpu_nvfp4(d), f"ffn nvfp4 run{run}", atol=FFN_ATOL)
+
+
+@pytest.fixture(scope="module")
+def cfg0():
+    return synth.cfg_ffn_fp8(0)
+
+
+def test_fp8_config0(cfg0):
+    need_gpu()
+    say("ffn fp8 cfg0 seed0")
+    gate(oracle_fp8(cfg0), gpu_fp8(cfg0), "ffn fp8 cfg0", atol=FFN_ATOL)
+
+
+def test_fp8_config0_literal_without_post_norm_and_gate(cfg0):
+    """BASELINE config 0 read literally: pre-RMSNorm -> GeGLU -> down -> residual add."""
+    need_gpu()
+    gate(oracle_fp8(cfg0, False, False), gpu_fp8(cfg0, False, False), "ffn fp8 cfg0 literal", atol=FFN_ATOL)
+
+
+def test_fp8_multi_row_and_determinism():
+    need_gpu()
+    d = synth.cfg_ffn_fp8(1, M=2)
+    a = gpu_fp8(d)
+    gate(oracle_fp8(d), a, "ffn fp8 M2", atol=FFN_ATOL)
+    assert np.array_equal(a, gpu_fp8(d))
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_mxfp4_config3(M):
+    need_gpu()
+    say(f"ffn mxfp4 cfg3 M{M}")
+    d = synth.cfg_ffn_mxfp4(0, M=M)
+    gate(oracle_mxfp4(d), gpu_mxfp4(d), f"ffn mxfp4 M{M}", atol=FFN_ATOL)
+
+
+def cancellation_residual(tiny_pow: int) -> np.ndarray:
+    """residual chunk [+1, -1, 478 x 2^p] per 480 (the QKV probe's construction,
+    qkv-boundary-probe-e53/generate_suite.py:48-49): after the pre-norm the large pair cancels
+    exactly in every projection row that weights it [1, 1, ...], leaving the tiny terms."""
+    x = np.full(3840, 2.0 ** tiny_pow, np.float32)
+    x[0::480], x[1::480] = 1.0, -1.0
+    return prng.f32_to_bf16_bits(x)
+
+
+@pytest.mark.parametrize("tiny_pow", [-23, -12])
+def test_fp8_and_mxfp4_cancellation_probes(tiny_pow):
+    """up . gelu(gate) partial sums near zero: up/gate rows weight the cancelling pair with +1,+1."""
+    need_gpu()
+    say(f"ffn cancellation probe 2^{tiny_pow}")
+    d = synth.cfg_ffn_fp8(4)
+    d["residual"] = cancellation_residual(tiny_pow)[None, :]
+    d["pre_ff_rms_weight"] = np.full(3840, 0x3F80, np.uint16)
+    for k in ("up_weight", "gate_weight"):
+        w = d[k].copy()
+        w[:, 0::480] = 0x38  # 1.0
+        w[:, 1::480] = 0x38
+        d[k] = w
+    gate(oracle_fp8(d), gpu_fp8(d), f"ffn fp8 cancel 2^{tiny_pow}", atol=FFN_ATOL)
+    m = synth.cfg_ffn_mxfp4(4)
+    m["residual"] = d["residual"]
+    m["pre_ff_rms_weight"] = d["pre_ff_rms_weight"]
+    gate(oracle_mxfp4(m), gpu_mxfp4(m), f"ffn mxfp4 cancel 2^{tiny_pow}", atol=FFN_ATOL)
