@@ -138,7 +138,7 @@ int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* 
                               int M, int N, int K, void* stream);
 
 /* Test support: decodes every E4M3 code, E2M1 byte, E8M0 code and bf16 GeLU input with the
- * kernels' own device helpers into out (device uint32 [66560]; layout in moa_decode.hip). */
+ * kernels' own device helpers into out (device uint32 [66564]; layout in moa_decode.hip). */
 int moa_format_selftest(uint32_t* out, void* stream);
 
 #ifdef __cplusplus

@@ -44,7 +44,7 @@ DevCtx* device_context(hipError_t* err) {
     if (c.base) return &c;
     size_t off = 0;
     auto carve = [&](size_t bytes) { size_t at = off; off = align_up(off + bytes, 256); return at; };
-    const size_t t_tickets = carve(sizeof(uint32_t) * kTicketCount);
+    const size_t t_tickets = carve(sizeof(uint32_t) * kTicketCount * kTicketStride);
     const size_t t_err = carve(sizeof(uint32_t) * 4);
     const size_t t_raw = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * (kQs + 2 * kPs));
     const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);

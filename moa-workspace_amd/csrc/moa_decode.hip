@@ -31,18 +31,87 @@ __device__ __forceinline__ float load_scale(const void* p, int i) {
     else return bf2f(static_cast<const uint16_t*>(p)[i]);
 }
 
-// Device-scope arrival counter. Returns true (in every lane) for the wave that arrives last
-// among `expected` arrivals; that wave then sees every other wave's stores. The counter
-// resets itself, so consecutive launches on one stream reuse it.
-__device__ __forceinline__ bool wave_arrive(uint32_t* ticket, uint32_t expected) {
-    __threadfence();  // release this wave's global stores (device scope)
-    uint32_t t = 0;
-    if (lane_id() == 0) t = atomicAdd(ticket, 1u);
-    t = __shfl(t, 0, kWave);
-    if (t + 1u != expected) return false;
-    __threadfence();  // acquire the other waves' stores
-    if (lane_id() == 0) atomicExch(ticket, 0u);
-    return true;
+// Cross-workgroup hand-off for the grid-wide epilogues.
+//
+// Workgroups publish() their results and then arrive on device-scope counters; the workgroup
+// that arrives last reads every result with collect(). Results are agent-scope atomic
+// stores/loads (global_store/load sc1 on gfx950: coherent across the XCDs' L2s without cache
+// maintenance). Each wave waits for its own stores to complete (s_waitcnt vmcnt(0)) before its
+// workgroup arrives, so a value is visible once the counters have counted its workgroup. No L2
+// writeback/invalidate is issued (a fence per wave costs more than these kernels' weight
+// stream), and each workgroup arrives once, on counters that never share a 256-byte line:
+// device-scope atomics to one line serialise. Counters reset themselves, so consecutive launches
+// on one stream reuse them.
+__device__ __forceinline__ void publish(uint16_t* p, uint32_t v) {
+    __hip_atomic_store(p, (uint16_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t collect(const uint16_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Eight published bf16 values (16 bytes) read coherently.
+__device__ __forceinline__ uint4 collect16(const uint16_t* p) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return make_uint4(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ uint32_t counter_add(uint32_t* c) {
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(uint32_t* c) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Whole block: true in every thread of the block that arrives last of `expected` on `ctr`.
+__device__ bool block_arrive(uint32_t* ctr, uint32_t expected) {
+    __shared__ uint32_t s_last;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's publishes are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const bool last = counter_add(ctr) + 1u == expected;
+        if (last) counter_reset(ctr);
+        s_last = last;
+    }
+    __syncthreads();
+    return s_last;
+}
+
+// Whole block: two-level arrival of all `nblocks` blocks of the grid row -- block b counts on
+// leaf b % kTreeLeaves; the last block of each leaf counts on the root. `tree` holds
+// kTreeCounters counters kTicketStride apart.
+__device__ bool block_arrive_tree(uint32_t* tree, uint32_t nblocks) {
+    __shared__ uint32_t s_last;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t leaf = blockIdx.x % kTreeLeaves;
+        const uint32_t n_leaf = (nblocks - leaf + kTreeLeaves - 1) / kTreeLeaves;
+        const uint32_t n_root = nblocks < (uint32_t)kTreeLeaves ? nblocks : (uint32_t)kTreeLeaves;
+        bool last = false;
+        uint32_t* lc = tree + leaf * kTicketStride;
+        if (counter_add(lc) + 1u == n_leaf) {
+            counter_reset(lc);
+            uint32_t* rc = tree + kTreeLeaves * kTicketStride;
+            last = counter_add(rc) + 1u == n_root;
+            if (last) counter_reset(rc);
+        }
+        s_last = last;
+    }
+    __syncthreads();
+    return s_last;
+}
+
+// Deterministic block sum (wave butterflies, then the four wave totals in order).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
 // h = RMSNorm(x, w) (gemma4.py:83-89) over kH elements into LDS as f32; w may be null.
@@ -132,32 +201,35 @@ __device__ __forceinline__ float dot_fp8_16(const float* x, const uint4& q, floa
     return acc;
 }
 
-__device__ __forceinline__ float dot_fp4_8(const float* x, uint32_t q, float scale, float acc) {
+// Eight E2M1 values (decoded at scale 1, exact) times x, accumulated onto acc.
+__device__ __forceinline__ float dot_fp4_8(const float* x, uint32_t q, float acc) {
     float w[8];
-    fp4x8_to_f32(q, scale, w);
+    fp4x8_to_f32(q, 1.0f, w);
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc = fmaf(x[t], w[t], acc);
     return acc;
 }
 
+// v_cvt_scalef32_pk_f32_fp4 applies only the exponent of its f32 scale (MX, E8M0 semantics),
+// so E2M1 codes are decoded at scale 1 and the block scale multiplies the block's partial sum:
+// exact for MXFP4's power-of-two scales; for NVFP4's E4M3 scales it adds one f32 rounding per
+// 16 elements to the reference's per-element fold (generate_references.py:398,407).
 template <FfnFormat F>
 __device__ __forceinline__ float chunk_dot(const float* x, const Chunk<F>& c, float acc) {
     if constexpr (F == FfnFormat::FP8) {
         return dot_fp8_16(x, c.q, acc);
     } else if constexpr (F == FfnFormat::NVFP4) {
-        // W = e2m1 * e4m3 block scale, exact in f32 (the reference folds it before the
-        // bf16 linear, generate_references.py:398,407).
-        f32x2 s = __builtin_amdgcn_cvt_pk_f32_fp8(c.s, false);
-        acc = dot_fp4_8(x, c.q.x, s[0], acc);
-        acc = dot_fp4_8(x + 8, c.q.y, s[0], acc);
-        acc = dot_fp4_8(x + 16, c.q.z, s[1], acc);
-        return dot_fp4_8(x + 24, c.q.w, s[1], acc);
+        f32x2 s = __builtin_amdgcn_cvt_pk_f32_fp8(c.s, false);  // two E4M3 block scales
+        float b0 = dot_fp4_8(x + 8, c.q.y, dot_fp4_8(x, c.q.x, 0.0f));
+        float b1 = dot_fp4_8(x + 24, c.q.w, dot_fp4_8(x + 16, c.q.z, 0.0f));
+        return fmaf(b1, s[1], fmaf(b0, s[0], acc));
     } else {
         const float s = e8m0_to_f32(c.s);
-        acc = dot_fp4_8(x, c.q.x, s, acc);
-        acc = dot_fp4_8(x + 8, c.q.y, s, acc);
-        acc = dot_fp4_8(x + 16, c.q.z, s, acc);
-        return dot_fp4_8(x + 24, c.q.w, s, acc);
+        float b = dot_fp4_8(x, c.q.x, 0.0f);
+        b = dot_fp4_8(x + 8, c.q.y, b);
+        b = dot_fp4_8(x + 16, c.q.z, b);
+        b = dot_fp4_8(x + 24, c.q.w, b);
+        return fmaf(b, s, acc);
     }
 }
 
@@ -173,30 +245,30 @@ __device__ __forceinline__ float proj_commit(float dot, float scale) {
 }
 
 // out[0:3840] = bf16(bf16(r + N(d)) * ls), N = RMSNorm with w_post or identity when null,
-// ls = layer scalar (skipped when null). One wave; 480 chunks of 8 elements, lane-strided.
+// ls = layer scalar (skipped when null). Whole block: 480 chunks of 8, thread t owns chunks t
+// and t + 256. d holds values published by other workgroups (read with collect16).
 // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241; oracle generate_references.py:411-413.
-__device__ void wave_post_residual(const uint16_t* __restrict__ d, const uint16_t* __restrict__ w_post,
-                                   uint16_t* __restrict__ r, const uint16_t* __restrict__ ls) {
-    const int lane = lane_id();
+__device__ void block_post_residual(const uint16_t* __restrict__ d, const uint16_t* __restrict__ w_post,
+                                    uint16_t* __restrict__ r, const uint16_t* __restrict__ ls) {
+    __shared__ float red[4];
     constexpr int NC = kH / 8;  // 480
-    constexpr int IT = (NC + kWave - 1) / kWave;  // 8
-    float dv[IT][8];
+    const int t = threadIdx.x;
+    float dv[2][8];
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const int c = i * kWave + lane;
+    for (int i = 0; i < 2; ++i) {
+        const int c = t + i * kBlock;
         if (c < NC) {
-            bf16x8_to_f32(ld16(d + c * 8), dv[i]);
+            bf16x8_to_f32(collect16(d + c * 8), dv[i]);
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss = fmaf(dv[i][e], dv[i][e], ss);
         }
     }
-    ss = wave_sum(ss);
-    const float inv = rms_inverse(ss, kH);
+    const float inv = rms_inverse(block_sum(ss, red), kH);
     const float lsv = ls ? bf2f(ls[0]) : 1.0f;
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const int c = i * kWave + lane;
+    for (int i = 0; i < 2; ++i) {
+        const int c = t + i * kBlock;
         if (c >= NC) continue;
         float wv[8], rv[8];
         if (w_post) bf16x8_to_f32(ld16(w_post + c * 8), wv);
@@ -206,10 +278,10 @@ __device__ void wave_post_residual(const uint16_t* __restrict__ d, const uint16_
         for (int e = 0; e < 8; ++e) {
             float n = dv[i][e];
             if (w_post) n = rbf((n * inv) * wv[e]);
-            float s = rbf(rv[e] + n);
-            if (ls) s = rbf(s * lsv);
-            const uint32_t b = f2bf(s);
-            if (e & 1) packed[e >> 1] |= b << 16; else packed[e >> 1] = b;
+            float sres = rbf(rv[e] + n);
+            if (ls) sres = rbf(sres * lsv);
+            const uint32_t bits = f2bf(sres);
+            if (e & 1) packed[e >> 1] |= bits << 16; else packed[e >> 1] = bits;
         }
         *reinterpret_cast<uint4*>(r + c * 8) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
     }
@@ -221,57 +293,44 @@ __device__ void wave_post_residual(const uint16_t* __restrict__ d, const uint16_
 constexpr int kQkvR = 4;
 constexpr int kQkvRows = kQs + 2 * kPs;
 
-// Per-head epilogue by the head's last wave: RMSNorm over 256 (sliding/rmsnorm.rs:22-153),
+// Per-head epilogue by the head's last workgroup: RMSNorm over 256 (sliding/rmsnorm.rs:22-153),
 // RoPE on q/k (sliding/rope.rs:9-211), and the q_out / ring-cache stores (ops.rs:72-75).
-// Lane l owns head elements {l, l+64, l+128, l+192}: RoPE partners (e, e+128) share a lane.
+// Thread t owns head element t; RoPE partners (t, t ^ 128) meet through LDS.
 __device__ void qkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict__ raw, int head,
                                   int m, uint32_t* err) {
-    const int lane = lane_id();
+    __shared__ float red[4];
+    __shared__ float xch[kDs];
+    const int t = threadIdx.x;
     const int32_t rope_off = *p.rope_off;
     const int32_t kv_off = *p.kv_off;
     const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + m < kE;
     const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
-    if ((head < 24 && !rope_ok) || (head >= 16 && !kv_ok)) {
-        if (lane == 0) atomicOr(err, rope_ok ? kErrKvOffset : kErrRopeOffset);
-        return;  // nothing is written when an offset is out of range
+    if (!rope_ok || !kv_ok) {  // the call writes nothing (no q_out, K or V) on a bad offset
+        if (t == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
+        return;
     }
     const int slot = (kv_off / (kNs * kDs * 2) + m) % kTs;
-    float v[4];
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = bf2f(raw[head * kDs + lane + 64 * i]);
-        ss = fmaf(v[i], v[i], ss);
-    }
-    const float inv = rms_inverse(wave_sum(ss), kDs);
+    const float v = bf2f(collect(&raw[head * kDs + t]));
+    const float inv = rms_inverse(block_sum(v * v, red), kDs);  // v*v is exact in f32
     const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
-    float n[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float y = v[i] * inv;
-        if (wn) y = y * bf2f(wn[lane + 64 * i]);
-        n[i] = rbf(y);
-    }
+    float n = v * inv;
+    if (wn) n = n * bf2f(wn[t]);
+    n = rbf(n);
     if (head >= 24) {
-        uint16_t* dst = p.v_cache + (size_t)slot * (kNs * kDs) + (head - 24) * kDs;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[lane + 64 * i] = (uint16_t)f2bf(n[i]);
+        p.v_cache[(size_t)slot * (kNs * kDs) + (head - 24) * kDs + t] = (uint16_t)f2bf(n);
         return;
     }
     // y = bf16(bf16(x*cos) + bf16(x_swap*sin_dev)); the table's sin has its low half negated
     // (generate_references.py:200-210), so x_swap is a plain half swap.
+    xch[t] = n;
+    __syncthreads();
+    const float partner = xch[t ^ (kDs / 2)];
     const int trow = rope_off / (kDs * 2) + m;
-    const uint16_t* cr = p.cos + (size_t)trow * kDs;
-    const uint16_t* sr = p.sin + (size_t)trow * kDs;
+    const float a = rbf(n * bf2f(p.cos[(size_t)trow * kDs + t]));
+    const float b = rbf(partner * bf2f(p.sin[(size_t)trow * kDs + t]));
     uint16_t* dst = head < 16 ? p.q_out + (size_t)m * kQs + head * kDs
                               : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        const float a = rbf(n[i] * bf2f(cr[e]));
-        const float b = rbf(n[(i + 2) & 3] * bf2f(sr[e]));
-        dst[e] = (uint16_t)f2bf(a + b);
-    }
+    dst[t] = (uint16_t)f2bf(a + b);
 }
 
 template <ScaleKind SK>
@@ -321,10 +380,10 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
         if (lane == r) mine = d;
     }
     uint16_t* raw = raw_all + (size_t)m * kQkvRows;
-    if (lane < R) raw[row0 + lane] = (uint16_t)f2bf(mine * load_scale<SK>(S, lr + lane));
+    if (lane < R) publish(&raw[row0 + lane], f2bf(mine * load_scale<SK>(S, lr + lane)));
 
-    const int head = row0 / kDs;  // 0..15 q, 16..23 k, 24..31 v
-    if (!wave_arrive(&tickets[kTicketQkv + m * 32 + head], kDs / R)) return;
+    const int head = row0 / kDs;  // 0..15 q, 16..23 k, 24..31 v (uniform over the block)
+    if (!block_arrive(&tickets[(kTicketQkv + m * 32 + head) * kTicketStride], kDs / (4 * R))) return;
     qkv_head_epilogue(p, raw, head, m0 + m, err);
 }
 
@@ -367,10 +426,10 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
         if (lane == r) mine = d;
     }
     uint16_t* pbuf = pbuf_all + (size_t)m * kH;
-    if (lane < R) pbuf[row0 + lane] = (uint16_t)f2bf(mine * load_scale<SK>(p.os, row0 + lane));
+    if (lane < R) publish(&pbuf[row0 + lane], f2bf(mine * load_scale<SK>(p.os, row0 + lane)));
 
-    if (!wave_arrive(&tickets[kTicketO + m], kH / R)) return;
-    wave_post_residual(pbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, nullptr);
+    if (!block_arrive_tree(&tickets[(kTicketO + m * kTreeCounters) * kTicketStride], gridDim.x)) return;
+    block_post_residual(pbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, nullptr);
 }
 
 // =================================================================== FFN
@@ -507,10 +566,10 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
         if (lane == r) mine = d;
     }
     uint16_t* dbuf = dbuf_all + (size_t)m * kH;
-    if (lane < R) dbuf[row0 + lane] = (uint16_t)f2bf(proj_commit<F>(mine, row_scale<F, SK>(p.down_s, p.down_g, row0 + lane)));
+    if (lane < R) publish(&dbuf[row0 + lane], f2bf(proj_commit<F>(mine, row_scale<F, SK>(p.down_s, p.down_g, row0 + lane))));
 
-    if (!wave_arrive(&tickets[kTicketFfn + m], kH / R)) return;
-    wave_post_residual(dbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, p.layer_scalar);
+    if (!block_arrive_tree(&tickets[(kTicketFfn + m * kTreeCounters) * kTicketStride], gridDim.x)) return;
+    block_post_residual(dbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, p.layer_scalar);
 }
 
 // ========================================================== raw projection
@@ -542,8 +601,16 @@ __global__ __launch_bounds__(kBlock) void proj_decode_kernel(ProjParams p) {
 //   out[256,768)      f32 bits of the two E2M1 nibbles of byte i (low nibble first)
 //   out[768,1024)     f32 bits of E8M0 code i
 //   out[1024,66560)   bf16 bits of bf16(gelu_tanh(bf16 value i))
+//   out[66560,66564)  f32 bits of the first E2M1 value of byte 0x77 (6.0) converted with the
+//                     f32 scale 15, 2, 3, 0.75 -- records how the hardware applies the scale
 __global__ void format_selftest_kernel(uint32_t* out) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 4) {
+        const float scales[4] = {15.0f, 2.0f, 3.0f, 0.75f};
+        float w[8];
+        fp4x8_to_f32(0x77u, scales[i], w);
+        out[66560 + i] = __float_as_uint(w[0]);
+    }
     if (i < 256) {
         float v[4];
         fp8x4_to_f32((uint32_t)i, v);

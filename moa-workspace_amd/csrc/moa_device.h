@@ -49,7 +49,8 @@ __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* o) {
 }
 
 // Eight E2M1 nibbles of one dword (low nibble = lower element index), each times `scale`.
-// The product e2m1 * scale is exact in f32 for E4M3 and power-of-two scales.
+// The hardware uses only the exponent of `scale` (a power-of-two MX scale); pass 1.0f for
+// plain decoding.
 __device__ __forceinline__ void fp4x8_to_f32(uint32_t w, float scale, float* o) {
     f32x2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
     f32x2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);

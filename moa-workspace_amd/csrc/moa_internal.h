@@ -13,11 +13,17 @@ constexpr int kMaxDecodeM = 16;
 // Rows handled by one call of the MFMA (M > kMaxDecodeM) path; larger calls are tiled by the host.
 constexpr int kMaxChunkM = 1024;
 
-// Ticket slots: [0, 32*kMaxDecodeM) QKV heads; then O; then FFN down.
+// Arrival counters. Each counter owns a 256-byte line: device-scope atomics to one line
+// serialise (~15 ns each), so counters never share a line and each kernel arrives once per
+// workgroup. Layout (in counters): [0, 32*kMaxDecodeM) QKV per (row, head);
+// then per row a 17-counter tree (16 leaves + 1 root) for O and again for the FFN down.
+constexpr int kTicketStride = 64;  // uint32 per counter (256 bytes)
+constexpr int kTreeLeaves = 16;
+constexpr int kTreeCounters = kTreeLeaves + 1;
 constexpr int kTicketQkv = 0;
 constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
-constexpr int kTicketFfn = kTicketO + kMaxDecodeM;
-constexpr int kTicketCount = kTicketFfn + kMaxDecodeM;
+constexpr int kTicketFfn = kTicketO + kTreeCounters * kMaxDecodeM;
+constexpr int kTicketCount = kTicketFfn + kTreeCounters * kMaxDecodeM;
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
@@ -27,7 +33,7 @@ constexpr uint32_t kErrSpinTimeout = 4u;
 // Per-device persistent scratch, allocated once on first use (never per call).
 struct DevCtx {
     int device = -1;
-    uint32_t* tickets = nullptr;  // kTicketCount, zero between calls (self-resetting)
+    uint32_t* tickets = nullptr;  // kTicketCount * kTicketStride, zero between calls (self-resetting)
     uint32_t* err = nullptr;      // 4 words
     uint16_t* raw_qkv = nullptr;  // [kMaxChunkM, 8192] bf16 raw projections
     uint16_t* pbuf = nullptr;     // [kMaxChunkM, 15360] bf16 (O: [M,3840]; FFN: GeGLU output)

@@ -126,9 +126,11 @@ def test_bad_offsets_write_nothing_and_raise_a_device_error():
         e = dict(d)
         e[field] = value
         ops.device_errors()  # clear
+        e["q_out"] = np.full(4096, 0x3FC0, np.uint16)
         q, kc, vc = run_gpu(e)
         assert ops.device_errors() & bit
         assert np.array_equal(kc, d["k_cache"]) and np.array_equal(vc, d["v_cache"])
+        assert np.all(q == 0x3FC0)
     assert ops.device_errors() == 0
 
 
