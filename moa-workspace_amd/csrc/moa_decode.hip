@@ -114,17 +114,39 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// h = RMSNorm(x, w) (gemma4.py:83-89) over kH elements into LDS as f32; w may be null.
-// Whole block. Thread t owns elements [16t, 16t+16) for t < 240.
-__device__ void stage_rmsnorm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                              float* __restrict__ lds, float* __restrict__ red) {
+// Activation staging in two phases: *_issue() loads the row into registers and must come
+// before the weight loads -- loads retire in order (vmcnt), so staging loads issued after a
+// wave's weight loads would make the LDS write wait for the whole weight stream -- and
+// *_finish() writes LDS once they arrive.
+
+// h = RMSNorm(x, w) (gemma4.py:83-89) over kH elements; w may be null. Thread t owns elements
+// [16t, 16t+16) for t < 240.
+struct RmsStage {
+    uint4 x0, x1, w0, w1;
+};
+
+__device__ __forceinline__ void rms_issue(RmsStage& s, const uint16_t* __restrict__ x,
+                                          const uint16_t* __restrict__ w) {
+    const int t = threadIdx.x;
+    if (t < kH / 16) {
+        s.x0 = ld16(x + t * 16);
+        s.x1 = ld16(x + t * 16 + 8);
+        if (w) {
+            s.w0 = ld16(w + t * 16);
+            s.w1 = ld16(w + t * 16 + 8);
+        }
+    }
+}
+
+// Whole block: finishes h into LDS as f32.
+__device__ void rms_finish(const RmsStage& s, bool weighted, float* __restrict__ lds, float* __restrict__ red) {
     const int t = threadIdx.x;
     const bool act = t < kH / 16;
     float xv[16];
     float ss = 0.0f;
     if (act) {
-        bf16x8_to_f32(ld16(x + t * 16), xv);
-        bf16x8_to_f32(ld16(x + t * 16 + 8), xv + 8);
+        bf16x8_to_f32(s.x0, xv);
+        bf16x8_to_f32(s.x1, xv + 8);
 #pragma unroll
         for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);  // x*x is exact in f32
     }
@@ -134,27 +156,48 @@ __device__ void stage_rmsnorm(const uint16_t* __restrict__ x, const uint16_t* __
     const float inv = rms_inverse(((red[0] + red[1]) + red[2]) + red[3], kH);
     if (act) {
         float wv[16];
-        if (w) {
-            bf16x8_to_f32(ld16(w + t * 16), wv);
-            bf16x8_to_f32(ld16(w + t * 16 + 8), wv + 8);
+        if (weighted) {
+            bf16x8_to_f32(s.w0, wv);
+            bf16x8_to_f32(s.w1, wv + 8);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float y = xv[i] * inv;
-            if (w) y = y * wv[i];
+            if (weighted) y = y * wv[i];
             lds[t * 16 + i] = rbf(y);
         }
     }
     __syncthreads();
 }
 
-// bf16 row of n elements (n % 8 == 0) into LDS as f32. Whole block.
-__device__ void stage_bf16(const uint16_t* __restrict__ x, int n, float* __restrict__ lds) {
-    for (int c = threadIdx.x; c < n / 8; c += kBlock) {
-        float v[8];
-        bf16x8_to_f32(ld16(x + c * 8), v);
+// A bf16 row of NC 8-element chunks, thread t owning chunks t + 256 i.
+template <int NC>
+struct RowStage {
+    static constexpr int N = (NC + kBlock - 1) / kBlock;
+    uint4 v[N];
+};
+
+template <int NC>
+__device__ __forceinline__ void row_issue(RowStage<NC>& s, const uint16_t* __restrict__ x) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lds[c * 8 + i] = v[i];
+    for (int i = 0; i < RowStage<NC>::N; ++i) {
+        const int c = threadIdx.x + i * kBlock;
+        if (c < NC) s.v[i] = ld16(x + c * 8);
+    }
+}
+
+// Whole block: the row into LDS as f32.
+template <int NC>
+__device__ void row_finish(const RowStage<NC>& s, float* __restrict__ lds) {
+#pragma unroll
+    for (int i = 0; i < RowStage<NC>::N; ++i) {
+        const int c = threadIdx.x + i * kBlock;
+        if (c < NC) {
+            float v[8];
+            bf16x8_to_f32(s.v[i], v);
+            *reinterpret_cast<f32x4*>(lds + c * 8) = f32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f32x4*>(lds + c * 8 + 4) = f32x4{v[4], v[5], v[6], v[7]};
+        }
     }
     __syncthreads();
 }
@@ -253,6 +296,17 @@ __device__ void block_post_residual(const uint16_t* __restrict__ d, const uint16
     __shared__ float red[4];
     constexpr int NC = kH / 8;  // 480
     const int t = threadIdx.x;
+    // Residual, post-norm weight and layer scalar first: their loads overlap the collect.
+    uint4 rq[2], wq[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = t + i * kBlock;
+        if (c < NC) {
+            rq[i] = ld16(r + c * 8);
+            if (w_post) wq[i] = ld16(w_post + c * 8);
+        }
+    }
+    const float lsv = ls ? bf2f(ls[0]) : 1.0f;
     float dv[2][8];
     float ss = 0.0f;
 #pragma unroll
@@ -265,14 +319,13 @@ __device__ void block_post_residual(const uint16_t* __restrict__ d, const uint16
         }
     }
     const float inv = rms_inverse(block_sum(ss, red), kH);
-    const float lsv = ls ? bf2f(ls[0]) : 1.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = t + i * kBlock;
         if (c >= NC) continue;
         float wv[8], rv[8];
-        if (w_post) bf16x8_to_f32(ld16(w_post + c * 8), wv);
-        bf16x8_to_f32(ld16(r + c * 8), rv);
+        if (w_post) bf16x8_to_f32(wq[i], wv);
+        bf16x8_to_f32(rq[i], rv);
         uint32_t packed[4];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -310,11 +363,16 @@ __device__ void qkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict
         return;
     }
     const int slot = (kv_off / (kNs * kDs * 2) + m) % kTs;
+    const int trow = rope_off / (kDs * 2) + m;
+    const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
+    // norm weight and RoPE row first: their loads overlap the collect
+    const float wv = wn ? bf2f(wn[t]) : 1.0f;
+    const float cv = bf2f(p.cos[(size_t)trow * kDs + t]);
+    const float sv = bf2f(p.sin[(size_t)trow * kDs + t]);
     const float v = bf2f(collect(&raw[head * kDs + t]));
     const float inv = rms_inverse(block_sum(v * v, red), kDs);  // v*v is exact in f32
-    const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
     float n = v * inv;
-    if (wn) n = n * bf2f(wn[t]);
+    if (wn) n = n * wv;
     n = rbf(n);
     if (head >= 24) {
         p.v_cache[(size_t)slot * (kNs * kDs) + (head - 24) * kDs + t] = (uint16_t)f2bf(n);
@@ -325,9 +383,8 @@ __device__ void qkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict
     xch[t] = n;
     __syncthreads();
     const float partner = xch[t ^ (kDs / 2)];
-    const int trow = rope_off / (kDs * 2) + m;
-    const float a = rbf(n * bf2f(p.cos[(size_t)trow * kDs + t]));
-    const float b = rbf(partner * bf2f(p.sin[(size_t)trow * kDs + t]));
+    const float a = rbf(n * cv);
+    const float b = rbf(partner * sv);
     uint16_t* dst = head < 16 ? p.q_out + (size_t)m * kQs + head * kDs
                               : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs;
     dst[t] = (uint16_t)f2bf(a + b);
@@ -349,6 +406,8 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
     else if (row0 < kQs + kPs) { W = p.kw; S = p.ks; lr = row0 - kQs; }
     else { W = p.vw; S = p.vs; lr = row0 - kQs - kPs; }
 
+    RmsStage st;
+    rms_issue(st, p.x + (size_t)(m0 + m) * kH, p.in_rms);
     uint4 wq[R][KI];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -358,7 +417,7 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
             wq[r][j] = (col < kH) ? ld_stream(W + (size_t)(lr + r) * kH + col) : make_uint4(0, 0, 0, 0);
         }
 
-    stage_rmsnorm(p.x + (size_t)(m0 + m) * kH, p.in_rms, hs, red);
+    rms_finish(st, true, hs, red);
 
     float acc[R];
 #pragma unroll
@@ -401,13 +460,15 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
     const int lane = lane_id(), wave = wave_id();
     const int row0 = blockIdx.x * (4 * R) + wave * R;
 
+    RowStage<kQs / 8> st;
+    row_issue(st, p.x + (size_t)(m0 + m) * kQs);
     uint4 wq[R][KI];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * kQs + j * 1024 + lane * 16);
 
-    stage_bf16(p.x + (size_t)(m0 + m) * kQs, kQs, xs);
+    row_finish(st, xs);
 
     float acc[R];
 #pragma unroll
@@ -480,9 +541,11 @@ __global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0
             }
         }
     };
+    RmsStage st;
+    rms_issue(st, p.residual + (size_t)(m0 + m) * kH, p.pre_rms);
     issue(0, ca);
 
-    stage_rmsnorm(p.residual + (size_t)(m0 + m) * kH, p.pre_rms, hs, red);
+    rms_finish(st, true, hs, red);
     float xv[KI][EPC];
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
@@ -535,6 +598,8 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
     const int lane = lane_id(), wave = wave_id();
     const int row0 = blockIdx.x * (4 * R) + wave * R;
 
+    RowStage<kL / 8> st;
+    row_issue(st, pbuf_all + (size_t)m * kL);
     Chunk<F> cb[R][KI];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -544,7 +609,7 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
                           p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
                           j * 1024 + lane * 16 < RB);
 
-    stage_bf16(pbuf_all + (size_t)m * kL, kL, ps);
+    row_finish(st, ps);
 
     float acc[R];
 #pragma unroll
