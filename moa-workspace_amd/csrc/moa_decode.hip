@@ -67,7 +67,7 @@ __device__ __forceinline__ void counter_reset(uint32_t* c) {
 }
 
 // Whole block: true in every thread of the block that arrives last of `expected` on `ctr`.
-__device__ bool block_arrive(uint32_t* ctr, uint32_t expected) {
+__device__ __forceinline__ bool block_arrive(uint32_t* ctr, uint32_t expected) {
     __shared__ uint32_t s_last;
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's publishes are done
     __syncthreads();
@@ -83,7 +83,7 @@ __device__ bool block_arrive(uint32_t* ctr, uint32_t expected) {
 // Whole block: two-level arrival of all `nblocks` blocks of the grid row -- block b counts on
 // leaf b % kTreeLeaves; the last block of each leaf counts on the root. `tree` holds
 // kTreeCounters counters kTicketStride apart.
-__device__ bool block_arrive_tree(uint32_t* tree, uint32_t nblocks) {
+__device__ __forceinline__ bool block_arrive_tree(uint32_t* tree, uint32_t nblocks) {
     __shared__ uint32_t s_last;
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -127,19 +127,17 @@ struct RmsStage {
 
 __device__ __forceinline__ void rms_issue(RmsStage& s, const uint16_t* __restrict__ x,
                                           const uint16_t* __restrict__ w) {
-    const int t = threadIdx.x;
-    if (t < kH / 16) {
-        s.x0 = ld16(x + t * 16);
-        s.x1 = ld16(x + t * 16 + 8);
-        if (w) {
-            s.w0 = ld16(w + t * 16);
-            s.w1 = ld16(w + t * 16 + 8);
-        }
+    const int t = min((int)threadIdx.x, kH / 16 - 1);  // threads past the row reload its last chunk
+    s.x0 = ld16(x + t * 16);
+    s.x1 = ld16(x + t * 16 + 8);
+    if (w) {
+        s.w0 = ld16(w + t * 16);
+        s.w1 = ld16(w + t * 16 + 8);
     }
 }
 
 // Whole block: finishes h into LDS as f32.
-__device__ void rms_finish(const RmsStage& s, bool weighted, float* __restrict__ lds, float* __restrict__ red) {
+__device__ __forceinline__ void rms_finish(const RmsStage& s, bool weighted, float* __restrict__ lds, float* __restrict__ red) {
     const int t = threadIdx.x;
     const bool act = t < kH / 16;
     float xv[16];
@@ -181,14 +179,14 @@ template <int NC>
 __device__ __forceinline__ void row_issue(RowStage<NC>& s, const uint16_t* __restrict__ x) {
 #pragma unroll
     for (int i = 0; i < RowStage<NC>::N; ++i) {
-        const int c = threadIdx.x + i * kBlock;
-        if (c < NC) s.v[i] = ld16(x + c * 8);
+        const int c = min((int)threadIdx.x + i * kBlock, NC - 1);  // clamped: no branch around the load
+        s.v[i] = ld16(x + c * 8);
     }
 }
 
 // Whole block: the row into LDS as f32.
 template <int NC>
-__device__ void row_finish(const RowStage<NC>& s, float* __restrict__ lds) {
+__device__ __forceinline__ void row_finish(const RowStage<NC>& s, float* __restrict__ lds) {
 #pragma unroll
     for (int i = 0; i < RowStage<NC>::N; ++i) {
         const int c = threadIdx.x + i * kBlock;
@@ -227,13 +225,18 @@ constexpr int elems_per_chunk() { return F == FfnFormat::FP8 ? 16 : 32; }
 template <FfnFormat F>
 __device__ __forceinline__ void load_chunk(Chunk<F>& c, const uint8_t* row, const uint8_t* srow,
                                            int j, int lane, bool valid) {
-    if (!valid) { c.q = make_uint4(0, 0, 0, 0); c.s = 0; return; }
-    c.q = ld_stream(row + j * 1024 + lane * 16);
+    // Invalid (past-the-row) lanes load the row's first chunk -- always in bounds, so the load
+    // needs no branch -- and zero it.
+    const int l = valid ? lane : 0;
+    const int jj = valid ? j : 0;
+    uint4 q = ld_stream(row + jj * 1024 + l * 16);
+    uint32_t sc = 0;
     if constexpr (F == FfnFormat::NVFP4)  // block 16: two E4M3 scale codes per chunk
-        c.s = *reinterpret_cast<const uint16_t*>(srow + (j * 64 + lane) * 2);
+        sc = *reinterpret_cast<const uint16_t*>(srow + (jj * 64 + l) * 2);
     else if constexpr (F == FfnFormat::MXFP4)  // block 32: one E8M0 scale code per chunk
-        c.s = srow[j * 64 + lane];
-    else c.s = 0;
+        sc = srow[jj * 64 + l];
+    c.q = valid ? q : make_uint4(0, 0, 0, 0);
+    c.s = valid ? sc : 0u;
 }
 
 __device__ __forceinline__ float dot_fp8_16(const float* x, const uint4& q, float acc) {
@@ -291,29 +294,29 @@ __device__ __forceinline__ float proj_commit(float dot, float scale) {
 // ls = layer scalar (skipped when null). Whole block: 480 chunks of 8, thread t owns chunks t
 // and t + 256. d holds values published by other workgroups (read with collect16).
 // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241; oracle generate_references.py:411-413.
-__device__ void block_post_residual(const uint16_t* __restrict__ d, const uint16_t* __restrict__ w_post,
+__device__ __forceinline__ void block_post_residual(const uint16_t* __restrict__ d, const uint16_t* __restrict__ w_post,
                                     uint16_t* __restrict__ r, const uint16_t* __restrict__ ls) {
     __shared__ float red[4];
     constexpr int NC = kH / 8;  // 480
     const int t = threadIdx.x;
     // Residual, post-norm weight and layer scalar first: their loads overlap the collect.
-    uint4 rq[2], wq[2];
+    // Clamped chunk indices keep every load unconditional, so all of them are in flight at once.
+    uint4 rq[2], wq[2], dq[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int c = t + i * kBlock;
-        if (c < NC) {
-            rq[i] = ld16(r + c * 8);
-            if (w_post) wq[i] = ld16(w_post + c * 8);
-        }
+        const int c = min(t + i * kBlock, NC - 1);
+        rq[i] = ld16(r + c * 8);
+        if (w_post) wq[i] = ld16(w_post + c * 8);
     }
     const float lsv = ls ? bf2f(ls[0]) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dq[i] = collect16(d + min(t + i * kBlock, NC - 1) * 8);
     float dv[2][8];
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int c = t + i * kBlock;
-        if (c < NC) {
-            bf16x8_to_f32(collect16(d + c * 8), dv[i]);
+        bf16x8_to_f32(dq[i], dv[i]);
+        if (t + i * kBlock < NC) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss = fmaf(dv[i][e], dv[i][e], ss);
         }
@@ -349,7 +352,7 @@ constexpr int kQkvRows = kQs + 2 * kPs;
 // Per-head epilogue by the head's last workgroup: RMSNorm over 256 (sliding/rmsnorm.rs:22-153),
 // RoPE on q/k (sliding/rope.rs:9-211), and the q_out / ring-cache stores (ops.rs:72-75).
 // Thread t owns head element t; RoPE partners (t, t ^ 128) meet through LDS.
-__device__ void qkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict__ raw, int head,
+__device__ __forceinline__ void qkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict__ raw, int head,
                                   int m, uint32_t* err) {
     __shared__ float red[4];
     __shared__ float xch[kDs];
@@ -406,6 +409,7 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
     else if (row0 < kQs + kPs) { W = p.kw; S = p.ks; lr = row0 - kQs; }
     else { W = p.vw; S = p.vs; lr = row0 - kQs - kPs; }
 
+    const float my_scale = load_scale<SK>(S, lr + min(lane, R - 1));  // lane r: row r's scale
     RmsStage st;
     rms_issue(st, p.x + (size_t)(m0 + m) * kH, p.in_rms);
     uint4 wq[R][KI];
@@ -414,7 +418,8 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
 #pragma unroll
         for (int j = 0; j < KI; ++j) {
             const int col = j * 1024 + lane * 16;
-            wq[r][j] = (col < kH) ? ld_stream(W + (size_t)(lr + r) * kH + col) : make_uint4(0, 0, 0, 0);
+            const uint4 q = ld_stream(W + (size_t)(lr + r) * kH + (col < kH ? col : 0));
+            wq[r][j] = (col < kH) ? q : make_uint4(0, 0, 0, 0);
         }
 
     rms_finish(st, true, hs, red);
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
         if (lane == r) mine = d;
     }
     uint16_t* raw = raw_all + (size_t)m * kQkvRows;
-    if (lane < R) publish(&raw[row0 + lane], f2bf(mine * load_scale<SK>(S, lr + lane)));
+    if (lane < R) publish(&raw[row0 + lane], f2bf(mine * my_scale));
 
     const int head = row0 / kDs;  // 0..15 q, 16..23 k, 24..31 v (uniform over the block)
     if (!block_arrive(&tickets[(kTicketQkv + m * 32 + head) * kTicketStride], kDs / (4 * R))) return;
@@ -460,6 +465,7 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
     const int lane = lane_id(), wave = wave_id();
     const int row0 = blockIdx.x * (4 * R) + wave * R;
 
+    const float my_scale = load_scale<SK>(p.os, row0 + min(lane, R - 1));
     RowStage<kQs / 8> st;
     row_issue(st, p.x + (size_t)(m0 + m) * kQs);
     uint4 wq[R][KI];
@@ -487,7 +493,7 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
         if (lane == r) mine = d;
     }
     uint16_t* pbuf = pbuf_all + (size_t)m * kH;
-    if (lane < R) publish(&pbuf[row0 + lane], f2bf(mine * load_scale<SK>(p.os, row0 + lane)));
+    if (lane < R) publish(&pbuf[row0 + lane], f2bf(mine * my_scale));
 
     if (!block_arrive_tree(&tickets[(kTicketO + m * kTreeCounters) * kTicketStride], gridDim.x)) return;
     block_post_residual(pbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, nullptr);
@@ -499,6 +505,7 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
 //   down:    p . W_down rows -> d[3840], then the last wave applies post-norm, residual and
 //            the layer scalar in place.
 constexpr int kUgRL = 8;   // L rows (an up row and a gate row each) per wave
+constexpr int kUgDepth = 4;  // up/gate pipeline ring depth
 constexpr int kDownR = 2;  // down rows per wave
 
 template <FfnFormat F>
@@ -521,29 +528,29 @@ __global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0
     constexpr int RB = row_bytes<F>(kH);
     constexpr int SB = scale_row_bytes<F>(kH);
     constexpr int KI = (RB + 1023) / 1024;
-    constexpr int RL = kUgRL, G = 1, NG = RL / G;
+    constexpr int RL = kUgRL;  // L rows per wave, one pipeline stage each (an up and a gate row)
+    constexpr int D = kUgDepth;  // stages in the ring: D - 1 rows stay in flight during compute
     const int m = blockIdx.y;
     const int lane = lane_id(), wave = wave_id();
     const int l0 = blockIdx.x * (4 * RL) + wave * RL;
 
-    // Two pipeline stages (A, B) of G L-rows each, in a loop the compiler does not unroll, so
-    // at most two stages of weight chunks are live per wave.
-    Chunk<F> ca[G][2][KI], cbb[G][2][KI];
-    auto issue = [&](int g, Chunk<F> (&dst)[G][2][KI]) {
+    Chunk<F> ring[D][2][KI];
+    auto issue = [&](int g, Chunk<F> (&dst)[2][KI]) {
+        const int l = l0 + g;
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
-            const int l = l0 + g * G + i;
-#pragma unroll
-            for (int j = 0; j < KI; ++j) {
-                const bool valid = j * 1024 + lane * 16 < RB;
-                load_chunk<F>(dst[i][0][j], p.up + (size_t)l * RB, (const uint8_t*)p.up_s + (size_t)l * SB, j, lane, valid);
-                load_chunk<F>(dst[i][1][j], p.gate + (size_t)l * RB, (const uint8_t*)p.gate_s + (size_t)l * SB, j, lane, valid);
-            }
+        for (int j = 0; j < KI; ++j) {
+            const bool valid = j * 1024 + lane * 16 < RB;
+            load_chunk<F>(dst[0][j], p.up + (size_t)l * RB, (const uint8_t*)p.up_s + (size_t)l * SB, j, lane, valid);
+            load_chunk<F>(dst[1][j], p.gate + (size_t)l * RB, (const uint8_t*)p.gate_s + (size_t)l * SB, j, lane, valid);
         }
     };
+    // lane i holds L-row l0+i's up and gate scales (FP8) or the global scales (NVFP4)
+    const float su = row_scale<F, SK>(p.up_s, p.up_g, l0 + min(lane, RL - 1));
+    const float sg = row_scale<F, SK>(p.gate_s, p.gate_g, l0 + min(lane, RL - 1));
     RmsStage st;
     rms_issue(st, p.residual + (size_t)(m0 + m) * kH, p.pre_rms);
-    issue(0, ca);
+#pragma unroll
+    for (int g = 0; g < D - 1; ++g) issue(g, ring[g]);
 
     rms_finish(st, true, hs, red);
     float xv[KI][EPC];
@@ -558,31 +565,25 @@ __global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0
     }
 
     uint16_t* pout = pbuf_all + (size_t)m * kL;
-    auto compute = [&](int g, const Chunk<F> (&src)[G][2][KI]) {
+    float pv = 0.0f;  // lane g keeps L-row l0+g's GeGLU output
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
-            float du = 0.0f, dg = 0.0f;
+    for (int g = 0; g < RL; ++g) {
+        if (g + D - 1 < RL) issue(g + D - 1, ring[(g + D - 1) % D]);
+        const Chunk<F> (&src)[2][KI] = ring[g % D];
+        float du = 0.0f, dg = 0.0f;
 #pragma unroll
-            for (int j = 0; j < KI; ++j) {
-                du = chunk_dot<F>(xv[j], src[i][0][j], du);
-                dg = chunk_dot<F>(xv[j], src[i][1][j], dg);
-            }
-            du = wave_sum(du);
-            dg = wave_sum(dg);
-            const int l = l0 + g * G + i;
-            const float up = proj_commit<F>(du, row_scale<F, SK>(p.up_s, p.up_g, l));
-            const float gate = proj_commit<F>(dg, row_scale<F, SK>(p.gate_s, p.gate_g, l));
-            // gemma4.py:197: bf16(bf16(gelu_tanh(gate)) * up)
-            if (lane == 0) pout[l] = (uint16_t)f2bf(rbf(gelu_tanh(gate)) * up);
+        for (int j = 0; j < KI; ++j) {
+            du = chunk_dot<F>(xv[j], src[0][j], du);
+            dg = chunk_dot<F>(xv[j], src[1][j], dg);
         }
-    };
-#pragma unroll 1
-    for (int g = 0; g < NG; g += 2) {
-        issue(g + 1, cbb);
-        compute(g, ca);
-        if (g + 2 < NG) issue(g + 2, ca);
-        compute(g + 1, cbb);
+        du = wave_sum(du);
+        dg = wave_sum(dg);
+        const float up = proj_commit<F>(du, __shfl(su, g, kWave));
+        const float gate = proj_commit<F>(dg, __shfl(sg, g, kWave));
+        // gemma4.py:197: bf16(bf16(gelu_tanh(gate)) * up)
+        if (lane == g) pv = rbf(gelu_tanh(gate)) * up;
     }
+    if (lane < RL) pout[l0 + lane] = (uint16_t)f2bf(pv);
 }
 
 template <FfnFormat F, ScaleKind SK>
@@ -598,6 +599,7 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
     const int lane = lane_id(), wave = wave_id();
     const int row0 = blockIdx.x * (4 * R) + wave * R;
 
+    const float my_scale = row_scale<F, SK>(p.down_s, p.down_g, row0 + min(lane, R - 1));
     RowStage<kL / 8> st;
     row_issue(st, pbuf_all + (size_t)m * kL);
     Chunk<F> cb[R][KI];
@@ -631,7 +633,7 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
         if (lane == r) mine = d;
     }
     uint16_t* dbuf = dbuf_all + (size_t)m * kH;
-    if (lane < R) publish(&dbuf[row0 + lane], f2bf(proj_commit<F>(mine, row_scale<F, SK>(p.down_s, p.down_g, row0 + lane))));
+    if (lane < R) publish(&dbuf[row0 + lane], f2bf(proj_commit<F>(mine, my_scale)));
 
     if (!block_arrive_tree(&tickets[(kTicketFfn + m * kTreeCounters) * kTicketStride], gridDim.x)) return;
     block_post_residual(dbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, p.layer_scalar);
