@@ -190,7 +190,7 @@ def main() -> int:
         "config": {"workload": "decode step, M=1: sliding_project_qkv (cfg2) + sliding_attention_output (cfg1) "
                                "+ decoder_feedforward FP8 (cfg0); weights rotated over >=512 MiB per operator",
                    "hidden": 3840, "intermediate": 15360, "tokens_per_step": 1},
-        "roofline": {"bound": "hbm", "kernel": "decoder_feedforward_fp8 (ffn_up_gate + ffn_down launches)",
+        "roofline": {"bound": "hbm", "kernel": "decoder_feedforward_fp8 (ffn_fused_kernel, one launch)",
                      "achieved": f["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": f["frac"],
                      "algorithmic_bytes": BYTES["ffn"], "avg_us": f["us"], "traffic": None},
         "ops": per_op,

@@ -50,6 +50,9 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);
     const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
+    int cus = 0;
+    *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (*err != hipSuccess) return nullptr;
     void* base = nullptr;
     *err = hipMalloc(&base, off);
     if (*err != hipSuccess) return nullptr;
@@ -61,6 +64,7 @@ DevCtx* device_context(hipError_t* err) {
     }
     char* b = static_cast<char*>(base);
     c.device = dev;
+    c.cus = cus;
     c.tickets = reinterpret_cast<uint32_t*>(b + t_tickets);
     c.err = reinterpret_cast<uint32_t*>(b + t_err);
     c.raw_qkv = reinterpret_cast<uint16_t*>(b + t_raw);

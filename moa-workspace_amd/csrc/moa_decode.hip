@@ -500,18 +500,22 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
 }
 
 // =================================================================== FFN
-// ops::decoder_feedforward (FO/src/ops.rs:201-239) in two launches:
-//   up_gate: pre-RMSNorm, up and gate rows, GeGLU -> p[15360] (bf16, scratch)
-//   down:    p . W_down rows -> d[3840], then the last wave applies post-norm, residual and
-//            the layer scalar in place.
-constexpr int kUgRL = 8;   // L rows (an up row and a gate row each) per wave
+// ops::decoder_feedforward (FO/src/ops.rs:201-239). Two halves:
+//   up_gate: pre-RMSNorm, up and gate rows, GeGLU -> p[15360] (bf16)
+//   down:    p . W_down rows -> d[3840], then post-norm, residual and the layer scalar in place.
+// One token row runs both halves in a single launch (ffn_fused_kernel) when its grid fits on the
+// device at once; otherwise, and for 2..16 rows (grid.y = row), they are two launches.
+// Activations (normalised x, p) are bf16 in LDS and enter the dot products as bf16 pairs.
+constexpr int kUgRL = 8;     // L rows (an up row and a gate row each) per wave
 constexpr int kUgDepth = 4;  // up/gate pipeline ring depth
-constexpr int kDownR = 2;  // down rows per wave
+constexpr int kDownR = 2;    // down rows per wave (two-launch path)
 
 template <FfnFormat F>
 constexpr int row_bytes(int k) { return F == FfnFormat::FP8 ? k : k / 2; }
 template <FfnFormat F>
 constexpr int scale_row_bytes(int k) { return F == FfnFormat::NVFP4 ? k / 16 : (F == FfnFormat::MXFP4 ? k / 32 : 0); }
+template <FfnFormat F>
+constexpr int down_chunks() { return (row_bytes<F>(kL) + 1023) / 1024; }
 
 template <FfnFormat F, ScaleKind SK>
 __device__ __forceinline__ float row_scale(const void* s, const float* g, int row) {
@@ -520,23 +524,88 @@ __device__ __forceinline__ float row_scale(const void* s, const float* g, int ro
     else return 1.0f;
 }
 
-template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0, uint16_t* pbuf_all) {
-    __shared__ float hs[kH];
-    __shared__ float red[4];
+// A chunk's dot with its EPC activations x[0 .. EPC/2) (bf16 pairs). FP4 block scales multiply
+// the block partial sums (see chunk_dot).
+template <FfnFormat F>
+__device__ __forceinline__ float chunk_dot2(const uint32_t* x, const Chunk<F>& c, float acc) {
+    if constexpr (F == FfnFormat::FP8) {
+        return dot_fp8x16_bf16(x, c.q, acc);
+    } else if constexpr (F == FfnFormat::NVFP4) {
+        f32x2 s = __builtin_amdgcn_cvt_pk_f32_fp8(c.s, false);  // two E4M3 block scales
+        float b0 = dot_fp4x8_bf16(x + 4, c.q.y, dot_fp4x8_bf16(x, c.q.x, 0.0f));
+        float b1 = dot_fp4x8_bf16(x + 12, c.q.w, dot_fp4x8_bf16(x + 8, c.q.z, 0.0f));
+        return fmaf(b1, s[1], fmaf(b0, s[0], acc));
+    } else {
+        float b = dot_fp4x8_bf16(x, c.q.x, 0.0f);
+        b = dot_fp4x8_bf16(x + 4, c.q.y, b);
+        b = dot_fp4x8_bf16(x + 8, c.q.z, b);
+        b = dot_fp4x8_bf16(x + 12, c.q.w, b);
+        return fmaf(b, e8m0_to_f32(c.s), acc);
+    }
+}
+
+// N bf16 activations at element `at` of an LDS row (16-byte aligned), as N/2 pairs.
+template <int N>
+__device__ __forceinline__ void lds_pairs(const uint16_t* lds, int at, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(lds + at + 8 * i);
+        out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+    }
+}
+
+// Whole block of NW waves: h = RMSNorm(x, w) from an RmsStage into LDS as bf16.
+template <int NW>
+__device__ __forceinline__ void rms_finish_bf16(const RmsStage& s, uint16_t* __restrict__ lds, float* __restrict__ red) {
+    const int t = threadIdx.x;
+    const bool act = t < kH / 16;
+    float xv[16];
+    float ss = 0.0f;
+    bf16x8_to_f32(s.x0, xv);
+    bf16x8_to_f32(s.x1, xv + 8);
+    if (act) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);  // x*x is exact in f32
+    }
+    ss = wave_sum(ss);
+    if (lane_id() == 0) red[wave_id()] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += red[w];
+    const float inv = rms_inverse(tot, kH);
+    if (act) {
+        float wv[16];
+        bf16x8_to_f32(s.w0, wv);
+        bf16x8_to_f32(s.w1, wv + 8);
+        uint32_t h[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(lds + t * 16) = make_uint4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<uint4*>(lds + t * 16 + 8) = make_uint4(h[4], h[5], h[6], h[7]);
+    }
+    __syncthreads();
+}
+
+// Pre-RMSNorm of the residual row x into hs (whole block of NW waves), then the wave's kUgRL
+// up/gate row pairs -- L-rows lbase + g*lstride, g < kUgRL -- through a D-deep ring of loads:
+// D - 1 row pairs stay in flight while one is reduced. Returns, in lane g < kUgRL, GeGLU of
+// L-row lbase + g*lstride (before its bf16 rounding).
+template <FfnFormat F, ScaleKind SK, int NW>
+__device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t* __restrict__ x, int lbase,
+                                              int lstride, uint16_t* __restrict__ hs, float* __restrict__ red) {
     constexpr int EPC = elems_per_chunk<F>();
     constexpr int RB = row_bytes<F>(kH);
     constexpr int SB = scale_row_bytes<F>(kH);
     constexpr int KI = (RB + 1023) / 1024;
-    constexpr int RL = kUgRL;  // L rows per wave, one pipeline stage each (an up and a gate row)
-    constexpr int D = kUgDepth;  // stages in the ring: D - 1 rows stay in flight during compute
-    const int m = blockIdx.y;
-    const int lane = lane_id(), wave = wave_id();
-    const int l0 = blockIdx.x * (4 * RL) + wave * RL;
+    constexpr int RL = kUgRL;
+    constexpr int D = kUgDepth;
+    const int lane = lane_id();
 
     Chunk<F> ring[D][2][KI];
     auto issue = [&](int g, Chunk<F> (&dst)[2][KI]) {
-        const int l = l0 + g;
+        const int l = lbase + g * lstride;
 #pragma unroll
         for (int j = 0; j < KI; ++j) {
             const bool valid = j * 1024 + lane * 16 < RB;
@@ -544,28 +613,32 @@ __global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0
             load_chunk<F>(dst[1][j], p.gate + (size_t)l * RB, (const uint8_t*)p.gate_s + (size_t)l * SB, j, lane, valid);
         }
     };
-    // lane i holds L-row l0+i's up and gate scales (FP8) or the global scales (NVFP4)
-    const float su = row_scale<F, SK>(p.up_s, p.up_g, l0 + min(lane, RL - 1));
-    const float sg = row_scale<F, SK>(p.gate_s, p.gate_g, l0 + min(lane, RL - 1));
-    RmsStage st;
-    rms_issue(st, p.residual + (size_t)(m0 + m) * kH, p.pre_rms);
+    // lane g holds L-row lbase+g*lstride's up and gate scales (FP8) or the global scales (NVFP4)
+    const int lrow = lbase + min(lane, RL - 1) * lstride;
+    const float su = row_scale<F, SK>(p.up_s, p.up_g, lrow);
+    const float sg = row_scale<F, SK>(p.gate_s, p.gate_g, lrow);
+    // The activation row (threads 0-239) goes first, and a barrier keeps every wave's weight
+    // loads behind it: a CU serves its waves' loads in order, so an activation load queued after
+    // another wave's weight ring would wait for that ring.
+    RmsStage st{};
+    if (wave_id() < 4) rms_issue(st, x, p.pre_rms);
+    __syncthreads();
 #pragma unroll
     for (int g = 0; g < D - 1; ++g) issue(g, ring[g]);
 
-    rms_finish(st, true, hs, red);
-    float xv[KI][EPC];
+    rms_finish_bf16<NW>(st, hs, red);
+    uint32_t xv[KI][EPC / 2];
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
         const int e0 = j * 64 * EPC + lane * EPC;
-        if (e0 < kH) lds_read<EPC>(hs, e0, xv[j]);
+        if (e0 < kH) lds_pairs<EPC>(hs, e0, xv[j]);
         else {
 #pragma unroll
-            for (int t = 0; t < EPC; ++t) xv[j][t] = 0.0f;
+            for (int t = 0; t < EPC / 2; ++t) xv[j][t] = 0u;
         }
     }
 
-    uint16_t* pout = pbuf_all + (size_t)m * kL;
-    float pv = 0.0f;  // lane g keeps L-row l0+g's GeGLU output
+    float pv = 0.0f;
 #pragma unroll
     for (int g = 0; g < RL; ++g) {
         if (g + D - 1 < RL) issue(g + D - 1, ring[(g + D - 1) % D]);
@@ -573,8 +646,8 @@ __global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0
         float du = 0.0f, dg = 0.0f;
 #pragma unroll
         for (int j = 0; j < KI; ++j) {
-            du = chunk_dot<F>(xv[j], src[0][j], du);
-            dg = chunk_dot<F>(xv[j], src[1][j], dg);
+            du = chunk_dot2<F>(xv[j], src[0][j], du);
+            dg = chunk_dot2<F>(xv[j], src[1][j], dg);
         }
         du = wave_sum(du);
         dg = wave_sum(dg);
@@ -583,60 +656,264 @@ __global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0
         // gemma4.py:197: bf16(bf16(gelu_tanh(gate)) * up)
         if (lane == g) pv = rbf(gelu_tanh(gate)) * up;
     }
-    if (lane < RL) pout[l0 + lane] = (uint16_t)f2bf(pv);
+    return pv;
 }
 
-template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, const uint16_t* pbuf_all,
-                                                          uint16_t* dbuf_all, uint32_t* tickets) {
-    __shared__ float ps[kL];  // 60 KB: two workgroups per CU
-    constexpr int EPC = elems_per_chunk<F>();
+// The wave's first n (<= R, uniform over the wave) down rows row0 .., every chunk's load issued
+// at once.
+template <FfnFormat F, int R>
+__device__ __forceinline__ void down_issue(Chunk<F> (&cb)[R][down_chunks<F>()], const FfnParams& p, int row0, int n,
+                                           int lane) {
     constexpr int RB = row_bytes<F>(kL);
     constexpr int SB = scale_row_bytes<F>(kL);
-    constexpr int KI = (RB + 1023) / 1024;
-    constexpr int R = kDownR;
-    const int m = blockIdx.y;
-    const int lane = lane_id(), wave = wave_id();
-    const int row0 = blockIdx.x * (4 * R) + wave * R;
-
-    const float my_scale = row_scale<F, SK>(p.down_s, p.down_g, row0 + min(lane, R - 1));
-    RowStage<kL / 8> st;
-    row_issue(st, pbuf_all + (size_t)m * kL);
-    Chunk<F> cb[R][KI];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r) {
+        if (r < n) {
 #pragma unroll
-        for (int j = 0; j < KI; ++j)
-            load_chunk<F>(cb[r][j], p.down + (size_t)(row0 + r) * RB,
-                          p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
-                          j * 1024 + lane * 16 < RB);
+            for (int j = 0; j < down_chunks<F>(); ++j)
+                load_chunk<F>(cb[r][j], p.down + (size_t)(row0 + r) * RB,
+                              p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
+                              j * 1024 + lane * 16 < RB);
+        }
+    }
+}
 
-    row_finish(st, ps);
-
+// Dots of the wave's first n down rows with p (bf16 in LDS); lane r < n returns row r's.
+template <FfnFormat F, int R>
+__device__ __forceinline__ float down_dots(const Chunk<F> (&cb)[R][down_chunks<F>()], const uint16_t* __restrict__ pl,
+                                           int n, int lane) {
+    constexpr int EPC = elems_per_chunk<F>();
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < KI; ++j) {
+    for (int j = 0; j < down_chunks<F>(); ++j) {
         const int e0 = j * 64 * EPC + lane * EPC;
         if (e0 < kL) {
-            float x[EPC];
-            lds_read<EPC>(ps, e0, x);
+            uint32_t x[EPC / 2];
+            lds_pairs<EPC>(pl, e0, x);
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = chunk_dot<F>(x, cb[r][j], acc[r]);
+            for (int r = 0; r < R; ++r)
+                if (r < n) acc[r] = chunk_dot2<F>(x, cb[r][j], acc[r]);
         }
     }
     float mine = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const float d = wave_sum(acc[r]);
-        if (lane == r) mine = d;
+        if (r < n) {
+            const float d = wave_sum(acc[r]);
+            if (lane == r) mine = d;
+        }
     }
+    return mine;
+}
+
+// ------------------------------------------------------------ two launches (2..16 token rows)
+template <FfnFormat F, ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0, uint16_t* pbuf_all) {
+    __shared__ uint16_t hs[kH];
+    __shared__ float red[4];
+    const int m = blockIdx.y;
+    const int lane = lane_id();
+    const int lbase = blockIdx.x * (4 * kUgRL) + wave_id();  // stage g: four consecutive rows
+    const float pv = up_gate_rows<F, SK, 4>(p, p.residual + (size_t)(m0 + m) * kH, lbase, 4, hs, red);
+    if (lane < kUgRL) pbuf_all[(size_t)m * kL + lbase + 4 * lane] = (uint16_t)f2bf(pv);
+}
+
+template <FfnFormat F, ScaleKind SK>
+__global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, const uint16_t* pbuf_all,
+                                                          uint16_t* dbuf_all, uint32_t* tickets) {
+    __shared__ uint16_t ps[kL];
+    const int m = blockIdx.y;
+    const int lane = lane_id();
+    const int row0 = blockIdx.x * (4 * kDownR) + wave_id() * kDownR;
+
+    const float my_scale = row_scale<F, SK>(p.down_s, p.down_g, row0 + min(lane, kDownR - 1));
+    RowStage<kL / 8> st;
+    row_issue(st, pbuf_all + (size_t)m * kL);
+    Chunk<F> cb[kDownR][down_chunks<F>()];
+    down_issue<F, kDownR>(cb, p, row0, kDownR, lane);
+#pragma unroll
+    for (int i = 0; i < RowStage<kL / 8>::N; ++i) {
+        const int c = threadIdx.x + i * kBlock;
+        if (c < kL / 8) *reinterpret_cast<uint4*>(ps + c * 8) = st.v[i];
+    }
+    __syncthreads();
+    const float mine = down_dots<F, kDownR>(cb, ps, kDownR, lane);
     uint16_t* dbuf = dbuf_all + (size_t)m * kH;
-    if (lane < R) publish(&dbuf[row0 + lane], f2bf(proj_commit<F>(mine, my_scale)));
+    if (lane < kDownR) publish(&dbuf[row0 + lane], f2bf(proj_commit<F>(mine, my_scale)));
 
     if (!block_arrive_tree(&tickets[(kTicketFfn + m * kTreeCounters) * kTicketStride], gridDim.x)) return;
     block_post_residual(dbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, p.layer_scalar);
+}
+
+// ------------------------------------------------------------ single launch (one token row)
+// Both halves in one grid of kFfnGrid workgroups of eight waves -- one workgroup per CU, so the
+// waves sharing a CU's memory path are symmetric -- that must all be resident at once (the host
+// checks the occupancy before choosing this kernel). Each workgroup computes 64 GeGLU values
+// (8 per wave; stage g of the ring reads eight consecutive L-rows, one per wave), then 16 down
+// rows (3, 3, 2, 2, 2, 2, 2 on waves 0-6), then those 16 residual outputs.
+//
+// Two grid-wide barriers: every down row needs all 15360 GeGLU values (p), and the post-norm of
+// every output needs the sum of squares of all 3840 down outputs. Waves 0-6 issue their down-row
+// loads before the first barrier, so the down weight stream follows the up/gate stream without a
+// gap. Wave 7 (the control wave) issues no down loads: loads retire in order, so a wave with
+// weight loads in flight would only see a barrier once they have landed. It publishes the
+// workgroup's GeGLU values, passes the barrier and stages p into LDS; after the down dots it
+// publishes the workgroup's partial sum of squares, passes the second barrier, sums the 240
+// partials in a fixed order (deterministic) and writes the workgroup's 16 outputs.
+//
+// A barrier is a 16-leaf arrival tree plus a generation word that moves by one per barrier: the
+// control wave reads it at entry (g0); the workgroup that completes a tree resets the tree and
+// stores g0 + k for barrier k; the others poll (agent-scope loads) until it reads g0 + k. The
+// poll is bounded by the wall clock (kSpinTicks): on expiry it sets kErrSpinTimeout in the device
+// error word and carries on, so every wave exits even if the grid were not resident.
+constexpr int kFfnWaves = 8;
+constexpr int kFfnBlock = 64 * kFfnWaves;
+constexpr int kFfnGrid = kL / (kFfnWaves * kUgRL);  // 240 workgroups
+constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgroup
+constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
+constexpr int kFfnDownR = 3;                        // down rows per wave (at most)
+static_assert(kFfnWgRows == 2 * 3 + 5 * 2, "down rows split 3, 3, 2, 2, 2, 2, 2 over waves 0-6");
+constexpr uint64_t kSpinTicks = 1ull << 24;  // ~168 ms of the 100 MHz wall clock
+
+__device__ __forceinline__ int ffn_down_first(int w) { return w < 2 ? 3 * w : 2 * w + 2; }
+__device__ __forceinline__ int ffn_down_count(int w) { return w < 2 ? 3 : (w < kFfnCtl ? 2 : 0); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+__device__ __forceinline__ void publish32(void* p, uint32_t v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Buffer resource over [base, base + bytes): loads past the end return zero instead of faulting.
+// Word 3 is the gfx9 raw-buffer setting (32-bit data format, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// One lane per workgroup, after its workgroup's results are published and complete: arrive on
+// `tree` (kTreeCounters counters kTicketStride apart) and wait until `gen` reads `target`.
+__device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint32_t target, uint32_t* err) {
+    const uint32_t leaf = blockIdx.x % kTreeLeaves;
+    const uint32_t n_leaf = (gridDim.x - leaf + kTreeLeaves - 1) / kTreeLeaves;
+    const uint32_t n_root = gridDim.x < (uint32_t)kTreeLeaves ? gridDim.x : (uint32_t)kTreeLeaves;
+    uint32_t* lc = tree + leaf * kTicketStride;
+    if (counter_add(lc) + 1u == n_leaf) {
+        counter_reset(lc);
+        uint32_t* rc = tree + kTreeLeaves * kTicketStride;
+        if (counter_add(rc) + 1u == n_root) {
+            counter_reset(rc);
+            __hip_atomic_store(gen, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    const uint64_t t0 = wall_clock64();
+    while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target) {
+        if (wall_clock64() - t0 > kSpinTicks) {
+            atomicOr(err, kErrSpinTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+template <FfnFormat F, ScaleKind SK>
+__global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, float* partials, uint32_t* tickets, uint32_t* err) {
+    __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
+    __shared__ float red[kFfnWaves];
+    __shared__ float pl[kFfnWaves * kUgRL];
+    __shared__ float dl[kFfnWgRows];
+    const int lane = lane_id(), wave = wave_id();
+    const bool ctl = wave == kFfnCtl;
+    uint32_t* gen = tickets + kTicketFfnGen * kTicketStride;
+    uint32_t g0 = 0;
+    if (ctl) g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint16_t* res = p.residual + (size_t)m0 * kH;
+    const bool post = p.post_rms != nullptr;
+
+    // down rows of this wave; the control wave's epilogue operands (lane i: output row i)
+    const int nd = ffn_down_count(wave);
+    const int drow0 = blockIdx.x * kFfnWgRows + ffn_down_first(wave);
+    const float dscale = row_scale<F, SK>(p.down_s, p.down_g, min(drow0 + min(lane, kFfnDownR - 1), kH - 1));
+    const int orow = blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1);
+    uint32_t r_bits = 0, w_bits = 0, ls_bits = 0;
+    if (ctl) {
+        r_bits = res[orow];
+        if (post) w_bits = p.post_rms[orow];
+        if (p.layer_scalar) ls_bits = p.layer_scalar[0];
+    }
+
+    // stage g reads L-rows base + 8g + wave: lane g's value is GeGLU row 8g + wave of the block
+    const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
+    const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red);
+    if (lane < kUgRL) pl[lane * kFfnWaves + wave] = pv;
+    __syncthreads();  // pl complete; every wave has read its x out of sh
+    // Down loads only once the whole workgroup is through its up/gate rows: issued earlier, they
+    // would queue ahead of the slower waves' up/gate loads (which the first barrier waits for).
+    Chunk<F> cb[kFfnDownR][down_chunks<F>()];
+    if (!ctl) down_issue<F, kFfnDownR>(cb, p, drow0, nd, lane);
+
+    if (ctl) {
+        if (lane < kFfnWaves * kUgRL / 2)
+            publish32(pbuf + blockIdx.x * (kFfnWaves * kUgRL) + 2 * lane,
+                      f2bf(pl[2 * lane]) | (f2bf(pl[2 * lane + 1]) << 16));
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // published before arriving
+        if (lane == 0) grid_barrier(tickets + kTicketFfnBar * kTicketStride, gen, g0 + 1u, err);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // no load below moves above the poll
+        // p into LDS straight from memory (no registers): 1920 chunks of 8, lane l moving chunks
+        // l + 64 i; agent-scope loads (sc1), like collect().
+#pragma unroll
+        for (int i = 0; i < kL / 8 / 64; ++i)
+            __builtin_amdgcn_global_load_lds((glb_void*)(pbuf + (lane + 64 * i) * 8), (lds_void*)(sh + 64 * 8 * i),
+                                             16, 0, 16 /* sc1 */);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();  // p staged
+
+    if (!ctl) {
+        const float d = down_dots<F, kFfnDownR>(cb, sh, nd, lane);
+        if (lane < nd) dl[ffn_down_first(wave) + lane] = bf2f(f2bf(proj_commit<F>(d, dscale)));
+    }
+    __syncthreads();  // dl complete
+
+    if (ctl) {
+        const float d = dl[min(lane, kFfnWgRows - 1)];
+        float inv = 1.0f;
+        if (post) {
+            // this workgroup's sum of squares, in row order, then all partials in a fixed order
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kFfnWgRows; ++i) ss = fmaf(dl[i], dl[i], ss);
+            if (lane == 0) publish32(partials + blockIdx.x, __float_as_uint(ss));
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (lane == 0) grid_barrier(tickets + kTicketFfn * kTicketStride, gen, g0 + 2u, err);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const __amdgpu_buffer_rsrc_t rq = coherent_rsrc(partials, kFfnGrid * sizeof(float));
+            constexpr int NP = (kFfnGrid + 63) / 64;
+            float part[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i)  // past the end reads zero
+                part[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, (lane + 64 * i) * 4, 0, 16 /* sc1 */));
+            float tot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NP; ++i) tot += part[i];
+            inv = rms_inverse(wave_sum(tot), kH);
+        }
+        // Without a post-norm there is nothing more to wait for: the first barrier already ordered
+        // every workgroup's read of the residual row before these writes, and the generation stays
+        // at g0 + 1 (the next launch reads it at entry). Nothing may store g0 + 2 here: a workgroup
+        // still polling the first barrier for g0 + 1 would then never see it.
+        if (lane < kFfnWgRows) {
+            // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241
+            float n = d;
+            if (post) n = rbf((n * inv) * bf2f(w_bits));
+            float sres = rbf(bf2f(r_bits) + n);
+            if (p.layer_scalar) sres = rbf(sres * bf2f(ls_bits));
+            res[orow] = (uint16_t)f2bf(sres);
+        }
+    }
 }
 
 // ========================================================== raw projection
@@ -723,11 +1000,31 @@ hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx) 
     return hipSuccess;
 }
 
+// Whether the single-launch FFN's grid fits on the device at once (checked once per device).
+template <FfnFormat F, ScaleKind SK>
+static bool ffn_fused_fits(DevCtx* ctx) {
+    int8_t& known = ctx->ffn_fused[(int)F * 2 + (int)SK];
+    if (known < 0) {
+        int per_cu = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, ffn_fused_kernel<F, SK>, kFfnBlock, 0);
+        known = (e == hipSuccess && per_cu * ctx->cus >= kFfnGrid) ? 1 : 0;
+    }
+    return known == 1;
+}
+
 template <FfnFormat F, ScaleKind SK>
 static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx) {
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
-        hipError_t e = launch(ffn_up_gate_kernel<F, SK>, dim3(kL / (4 * kUgRL), mm), s, p, m0, ctx->pbuf);
+        hipError_t e;
+        if (mm == 1 && ffn_fused_fits<F, SK>(ctx)) {
+            ffn_fused_kernel<F, SK><<<dim3(kFfnGrid), dim3(kFfnBlock), 0, s>>>(
+                p, m0, ctx->pbuf, reinterpret_cast<float*>(ctx->dbuf), ctx->tickets, ctx->err);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            continue;
+        }
+        e = launch(ffn_up_gate_kernel<F, SK>, dim3(kL / (4 * kUgRL), mm), s, p, m0, ctx->pbuf);
         if (e != hipSuccess) return e;
         e = launch(ffn_down_kernel<F, SK>, dim3(kH / (4 * kDownR), mm), s, p, m0,
                    (const uint16_t*)ctx->pbuf, ctx->dbuf, ctx->tickets);

@@ -60,6 +60,37 @@ __device__ __forceinline__ void fp4x8_to_f32(uint32_t w, float scale, float* o) 
     o[4] = c[0]; o[5] = c[1]; o[6] = d[0]; o[7] = d[1];
 }
 
+// ------------------------------------------------- bf16 dot products (FFN)
+// Activations stay bf16, two per dword (lower element in the low half); weights widen to bf16
+// exactly (E4M3 and E2M1 values are bf16 values; the conversions run at scale 1) and
+// v_dot2c_f32_bf16 accumulates acc + a.lo*b.lo + a.hi*b.hi in f32 -- bf16 x bf16 products are
+// exact in f32, so only the accumulation order differs from a chain of fmaf().
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t x2, bf16x2 w2, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x2), w2, acc, false);
+}
+
+// 16 E4M3 codes (a 16-byte chunk) against 16 activations x[0..8) (pairs).
+__device__ __forceinline__ float dot_fp8x16_bf16(const uint32_t* x, const uint4& q, float acc) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc = dot2_bf16(x[2 * i], __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, false), acc);
+        acc = dot2_bf16(x[2 * i + 1], __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[i], 1.0f, true), acc);
+    }
+    return acc;
+}
+
+// 8 E2M1 codes (one dword, low nibble first) against 8 activations x[0..4) (pairs).
+__device__ __forceinline__ float dot_fp4x8_bf16(const uint32_t* x, uint32_t w, float acc) {
+    acc = dot2_bf16(x[0], __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 0), acc);
+    acc = dot2_bf16(x[1], __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 1), acc);
+    acc = dot2_bf16(x[2], __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 2), acc);
+    acc = dot2_bf16(x[3], __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, 3), acc);
+    return acc;
+}
+
 __device__ __forceinline__ float e4m3_to_f32(uint32_t code) {
     return __builtin_amdgcn_cvt_pk_f32_fp8(code & 0xffu, false)[0];
 }

@@ -16,14 +16,17 @@ constexpr int kMaxChunkM = 1024;
 // Arrival counters. Each counter owns a 256-byte line: device-scope atomics to one line
 // serialise (~15 ns each), so counters never share a line and each kernel arrives once per
 // workgroup. Layout (in counters): [0, 32*kMaxDecodeM) QKV per (row, head);
-// then per row a 17-counter tree (16 leaves + 1 root) for O and again for the FFN down.
+// then per row a 17-counter tree (16 leaves + 1 root) for O and again for the FFN down; then the
+// grid barrier of the single-launch FFN (a 17-counter tree and a generation word).
 constexpr int kTicketStride = 64;  // uint32 per counter (256 bytes)
 constexpr int kTreeLeaves = 16;
 constexpr int kTreeCounters = kTreeLeaves + 1;
 constexpr int kTicketQkv = 0;
 constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
 constexpr int kTicketFfn = kTicketO + kTreeCounters * kMaxDecodeM;
-constexpr int kTicketCount = kTicketFfn + kTreeCounters * kMaxDecodeM;
+constexpr int kTicketFfnBar = kTicketFfn + kTreeCounters * kMaxDecodeM;
+constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
+constexpr int kTicketCount = kTicketFfnGen + 1;
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
@@ -40,6 +43,8 @@ struct DevCtx {
     uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
     void* base = nullptr;
+    int cus = 0;                  // compute units of the device
+    int8_t ffn_fused[6] = {-1, -1, -1, -1, -1, -1};  // per (format, scale kind): grid fits resident? (-1 unknown)
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
