@@ -50,6 +50,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);
     const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
+    const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
     int cus = 0;
     *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (*err != hipSuccess) return nullptr;
@@ -71,6 +72,7 @@ DevCtx* device_context(hipError_t* err) {
     c.pbuf = reinterpret_cast<uint16_t*>(b + t_p);
     c.dbuf = reinterpret_cast<uint16_t*>(b + t_d);
     c.hbuf = reinterpret_cast<uint16_t*>(b + t_h);
+    c.ffn_part = reinterpret_cast<uint64_t*>(b + t_part);
     c.base = base;
     return &c;
 }

@@ -507,7 +507,8 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
 // device at once; otherwise, and for 2..16 rows (grid.y = row), they are two launches.
 // Activations (normalised x, p) are bf16 in LDS and enter the dot products as bf16 pairs.
 constexpr int kUgRL = 8;     // L rows (an up row and a gate row each) per wave
-constexpr int kUgDepth = 4;  // up/gate pipeline ring depth
+constexpr int kUgDepth = 2;  // up/gate pipeline ring depth
+constexpr int kUgPre = 1;    // ring stages issued before the pre-norm completes (<= kUgDepth - 1)
 constexpr int kDownR = 2;    // down rows per wave (two-launch path)
 
 template <FfnFormat F>
@@ -620,13 +621,17 @@ __device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t
     // The activation row (threads 0-239) goes first, and a barrier keeps every wave's weight
     // loads behind it: a CU serves its waves' loads in order, so an activation load queued after
     // another wave's weight ring would wait for that ring.
+    // Only kUgPre stages go out before the pre-norm completes: a wave's issue stalls once its
+    // CU's load queue is full, and the norm's barriers wait for every wave.
     RmsStage st{};
     if (wave_id() < 4) rms_issue(st, x, p.pre_rms);
     __syncthreads();
 #pragma unroll
-    for (int g = 0; g < D - 1; ++g) issue(g, ring[g]);
+    for (int g = 0; g < kUgPre; ++g) issue(g, ring[g]);
 
     rms_finish_bf16<NW>(st, hs, red);
+#pragma unroll
+    for (int g = kUgPre; g < D - 1; ++g) issue(g, ring[g]);
     uint32_t xv[KI][EPC / 2];
 #pragma unroll
     for (int j = 0; j < KI; ++j) {
@@ -676,6 +681,20 @@ __device__ __forceinline__ void down_issue(Chunk<F> (&cb)[R][down_chunks<F>()], 
                               j * 1024 + lane * 16 < RB);
         }
     }
+}
+
+// Chunk j of each of the wave's first n (<= R, uniform over the wave) down rows row0 ...
+template <FfnFormat F, int R>
+__device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnParams& p, int row0, int n, int j,
+                                                 int lane) {
+    constexpr int RB = row_bytes<F>(kL);
+    constexpr int SB = scale_row_bytes<F>(kL);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < n)
+            load_chunk<F>(dst[r], p.down + (size_t)(row0 + r) * RB,
+                          p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
+                          j * 1024 + lane * 16 < RB);
 }
 
 // Dots of the wave's first n down rows with p (bf16 in LDS); lane r < n returns row r's.
@@ -752,33 +771,41 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
 // waves sharing a CU's memory path are symmetric -- that must all be resident at once (the host
 // checks the occupancy before choosing this kernel). Each workgroup computes 64 GeGLU values
 // (8 per wave; stage g of the ring reads eight consecutive L-rows, one per wave), then 16 down
-// rows (3, 3, 2, 2, 2, 2, 2 on waves 0-6), then those 16 residual outputs.
+// rows (2 per wave).
 //
-// Two grid-wide barriers: every down row needs all 15360 GeGLU values (p), and the post-norm of
-// every output needs the sum of squares of all 3840 down outputs. Waves 0-6 issue their down-row
-// loads before the first barrier, so the down weight stream follows the up/gate stream without a
-// gap. Wave 7 (the control wave) issues no down loads: loads retire in order, so a wave with
-// weight loads in flight would only see a barrier once they have landed. It publishes the
-// workgroup's GeGLU values, passes the barrier and stages p into LDS; after the down dots it
-// publishes the workgroup's partial sum of squares, passes the second barrier, sums the 240
-// partials in a fixed order (deterministic) and writes the workgroup's 16 outputs.
+// Two grid-wide dependencies: every down row needs all 15360 GeGLU values (p), and the post-norm
+// of every output needs the sum of squares of all 3840 down outputs.
 //
-// A barrier is a 16-leaf arrival tree plus a generation word that moves by one per barrier: the
-// control wave reads it at entry (g0); the workgroup that completes a tree resets the tree and
-// stores g0 + k for barrier k; the others poll (agent-scope loads) until it reads g0 + k. The
-// poll is bounded by the wall clock (kSpinTicks): on expiry it sets kErrSpinTimeout in the device
-// error word and carries on, so every wave exits even if the grid were not resident.
+// p: wave 7 (the control wave) publishes the workgroup's GeGLU values and arrives on a barrier --
+// a 16-leaf arrival tree plus a generation word that moves by one per launch: the control wave
+// reads it at entry (g0); the workgroup that completes the tree resets the tree and stores
+// g0 + 1; the others poll until it reads g0 + 1 -- then stages p into LDS. Waves 0-6 issue the
+// first kFfnDownPre chunks of their down rows before the barrier, so the down weight stream
+// follows the up/gate stream. The control wave issues its own down loads only after staging p:
+// a CU serves its loads in order, so a wave with weight loads in flight would see the barrier
+// only once they had landed.
+//
+// Post-norm: every workgroup publishes its 16 down outputs and its partial sum of squares, each
+// 64-bit word tagged with g0 + 1 (a word holding the tag is complete, so no counters), and is
+// done. The kFfnLeaders leader workgroups poll the tags: leader g sums all 240 partials in a fixed
+// order (deterministic, the same bits in every leader) and writes the outputs of the workgroups
+// b = g (mod kFfnLeaders). Few pollers keep the tagged lines free of contention.
+//
+// Every poll is bounded by the wall clock (kSpinTicks): on expiry it sets kErrSpinTimeout in the
+// device error word and carries on, so every wave exits even if the grid were not resident.
 constexpr int kFfnWaves = 8;
 constexpr int kFfnBlock = 64 * kFfnWaves;
 constexpr int kFfnGrid = kL / (kFfnWaves * kUgRL);  // 240 workgroups
 constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgroup
 constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
-constexpr int kFfnDownR = 3;                        // down rows per wave (at most)
-static_assert(kFfnWgRows == 2 * 3 + 5 * 2, "down rows split 3, 3, 2, 2, 2, 2, 2 over waves 0-6");
+constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
+constexpr int kFfnDownPre = 6;                      // down chunks per row loaded before the first barrier
+constexpr int kFfnLeaders = 8;                      // workgroups that finish the post-norm
+constexpr int kFfnGroup = kFfnGrid / kFfnLeaders;   // 30 workgroups per leader
+static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
+static_assert(kFfnGroup * kFfnLeaders == kFfnGrid && 2 * kFfnGroup <= 64, "a leader lane owns 8 outputs");
+static_assert(kFfnGrid <= kFfnPartSlots, "one tagged partial slot per workgroup");
 constexpr uint64_t kSpinTicks = 1ull << 24;  // ~168 ms of the 100 MHz wall clock
-
-__device__ __forceinline__ int ffn_down_first(int w) { return w < 2 ? 3 * w : 2 * w + 2; }
-__device__ __forceinline__ int ffn_down_count(int w) { return w < 2 ? 3 : (w < kFfnCtl ? 2 : 0); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
@@ -786,11 +813,11 @@ typedef __attribute__((address_space(1))) void glb_void;
 __device__ __forceinline__ void publish32(void* p, uint32_t v) {
     __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-// Buffer resource over [base, base + bytes): loads past the end return zero instead of faulting.
-// Word 3 is the gfx9 raw-buffer setting (32-bit data format, no swizzle).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+__device__ __forceinline__ void publish64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t collect64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One lane per workgroup, after its workgroup's results are published and complete: arrive on
@@ -818,44 +845,66 @@ __device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint
     }
 }
 
+// Tagged hand-off area of the single-launch FFN: per workgroup one partial-sum word (f32 bits |
+// tag << 32) and eight down-output words (two bf16 outputs | tag << 32).
+struct FfnSlots {
+    uint64_t part[kFfnPartSlots];
+    uint64_t d[kFfnPartSlots][kFfnWgRows / 2];
+};
+
 template <FfnFormat F, ScaleKind SK>
 __global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, float* partials, uint32_t* tickets, uint32_t* err) {
+void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, FfnSlots* slots, uint32_t* tickets, uint32_t* err) {
+    constexpr int KD = down_chunks<F>();
+    constexpr int EPC = elems_per_chunk<F>();
     __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
     __shared__ float red[kFfnWaves];
     __shared__ float pl[kFfnWaves * kUgRL];
-    __shared__ float dl[kFfnWgRows];
+    __shared__ uint32_t dl[kFfnWgRows];  // the workgroup's down outputs (bf16 bits)
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
+    const bool leader = blockIdx.x < kFfnLeaders;
     uint32_t* gen = tickets + kTicketFfnGen * kTicketStride;
     uint32_t g0 = 0;
     if (ctl) g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint16_t* res = p.residual + (size_t)m0 * kH;
     const bool post = p.post_rms != nullptr;
 
-    // down rows of this wave; the control wave's epilogue operands (lane i: output row i)
-    const int nd = ffn_down_count(wave);
-    const int drow0 = blockIdx.x * kFfnWgRows + ffn_down_first(wave);
-    const float dscale = row_scale<F, SK>(p.down_s, p.down_g, min(drow0 + min(lane, kFfnDownR - 1), kH - 1));
-    const int orow = blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1);
-    uint32_t r_bits = 0, w_bits = 0, ls_bits = 0;
+    const int drow0 = blockIdx.x * kFfnWgRows + wave * kFfnDownR;
+    const float dscale = row_scale<F, SK>(p.down_s, p.down_g, drow0 + min(lane, kFfnDownR - 1));
+
+    // Epilogue operands of the control wave, fetched now (off the critical path). With a post-norm
+    // a leader's lane l < 2 * kFfnGroup owns 8 outputs of workgroup g + 8 (l / 2), rows
+    // (l % 2) * 8 ..; without one, every workgroup writes its own 16 outputs (lanes 0-15).
+    uint4 r8 = make_uint4(0, 0, 0, 0), w8 = make_uint4(0, 0, 0, 0);
+    uint32_t r1 = 0, ls_bits = 0;
+    const int lwg = blockIdx.x + kFfnLeaders * min(lane / 2, kFfnGroup - 1);  // leader: workgroup of lane
+    const int lrow = lwg * kFfnWgRows + (lane % 2) * 8;
     if (ctl) {
-        r_bits = res[orow];
-        if (post) w_bits = p.post_rms[orow];
         if (p.layer_scalar) ls_bits = p.layer_scalar[0];
+        if (post && leader) {
+            r8 = ld16(res + lrow);
+            w8 = ld16(p.post_rms + lrow);
+        } else if (!post) {
+            r1 = res[blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1)];
+        }
     }
 
-    // stage g reads L-rows base + 8g + wave: lane g's value is GeGLU row 8g + wave of the block
+    // ---- up/gate: stage g reads L-rows base + 8g + wave; lane g's value is GeGLU row 8g + wave
     const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
     const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red);
     if (lane < kUgRL) pl[lane * kFfnWaves + wave] = pv;
     __syncthreads();  // pl complete; every wave has read its x out of sh
-    // Down loads only once the whole workgroup is through its up/gate rows: issued earlier, they
-    // would queue ahead of the slower waves' up/gate loads (which the first barrier waits for).
-    Chunk<F> cb[kFfnDownR][down_chunks<F>()];
-    if (!ctl) down_issue<F, kFfnDownR>(cb, p, drow0, nd, lane);
 
-    if (ctl) {
+    // Down loads only once the whole workgroup is through its up/gate rows (issued earlier they
+    // would queue ahead of the slower waves' up/gate loads, which the barrier waits for).
+    constexpr int PD = kFfnDownPre < KD ? kFfnDownPre : KD;
+    constexpr int RS = PD < KD ? PD + 1 : KD;  // ring slots
+    Chunk<F> ring[RS][kFfnDownR];
+    if (!ctl) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
+    } else {
         if (lane < kFfnWaves * kUgRL / 2)
             publish32(pbuf + blockIdx.x * (kFfnWaves * kUgRL) + 2 * lane,
                       f2bf(pl[2 * lane]) | (f2bf(pl[2 * lane + 1]) << 16));
@@ -872,47 +921,110 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, float* partials, uint
     }
     __syncthreads();  // p staged
 
-    if (!ctl) {
-        const float d = down_dots<F, kFfnDownR>(cb, sh, nd, lane);
-        if (lane < nd) dl[ffn_down_first(wave) + lane] = bf2f(f2bf(proj_commit<F>(d, dscale)));
+    // ---- down: the ring streams the rest of the rows while the dots run
+    if (ctl) {  // issued after the barrier so that no other wave waits on these issues
+#pragma unroll
+        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
+    }
+    {
+        float acc[kFfnDownR];
+#pragma unroll
+        for (int r = 0; r < kFfnDownR; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KD; ++j) {
+            if (j + PD < KD) down_chunk_issue<F, kFfnDownR>(ring[(j + PD) % RS], p, drow0, kFfnDownR, j + PD, lane);
+            const int e0 = j * 64 * EPC + lane * EPC;
+            if (e0 < kL) {
+                uint32_t x[EPC / 2];
+                lds_pairs<EPC>(sh, e0, x);
+#pragma unroll
+                for (int r = 0; r < kFfnDownR; ++r) acc[r] = chunk_dot2<F>(x, ring[j % RS][r], acc[r]);
+            }
+        }
+        float mine = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kFfnDownR; ++r) {
+            const float dsum = wave_sum(acc[r]);
+            if (lane == r) mine = dsum;
+        }
+        if (lane < kFfnDownR) dl[wave * kFfnDownR + lane] = f2bf(proj_commit<F>(mine, dscale));
     }
     __syncthreads();  // dl complete
+    if (!ctl) return;
 
-    if (ctl) {
-        const float d = dl[min(lane, kFfnWgRows - 1)];
-        float inv = 1.0f;
-        if (post) {
-            // this workgroup's sum of squares, in row order, then all partials in a fixed order
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < kFfnWgRows; ++i) ss = fmaf(dl[i], dl[i], ss);
-            if (lane == 0) publish32(partials + blockIdx.x, __float_as_uint(ss));
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            if (lane == 0) grid_barrier(tickets + kTicketFfn * kTicketStride, gen, g0 + 2u, err);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const __amdgpu_buffer_rsrc_t rq = coherent_rsrc(partials, kFfnGrid * sizeof(float));
-            constexpr int NP = (kFfnGrid + 63) / 64;
-            float part[NP];
-#pragma unroll
-            for (int i = 0; i < NP; ++i)  // past the end reads zero
-                part[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, (lane + 64 * i) * 4, 0, 16 /* sc1 */));
-            float tot = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NP; ++i) tot += part[i];
-            inv = rms_inverse(wave_sum(tot), kH);
-        }
-        // Without a post-norm there is nothing more to wait for: the first barrier already ordered
-        // every workgroup's read of the residual row before these writes, and the generation stays
-        // at g0 + 1 (the next launch reads it at entry). Nothing may store g0 + 2 here: a workgroup
-        // still polling the first barrier for g0 + 1 would then never see it.
+    // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241: out = bf16(bf16(r + n) * ls),
+    // n = bf16(bf16(d * inv) * w) with the post-norm, n = d without it.
+    const float lsv = p.layer_scalar ? bf2f(ls_bits) : 1.0f;
+    if (!post) {
+        // Nothing to wait for: the barrier already ordered every workgroup's read of the residual
+        // row before these writes.
         if (lane < kFfnWgRows) {
-            // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241
-            float n = d;
-            if (post) n = rbf((n * inv) * bf2f(w_bits));
-            float sres = rbf(bf2f(r_bits) + n);
-            if (p.layer_scalar) sres = rbf(sres * bf2f(ls_bits));
-            res[orow] = (uint16_t)f2bf(sres);
+            float sres = rbf(bf2f(r1) + bf2f(dl[lane]));
+            if (p.layer_scalar) sres = rbf(sres * lsv);
+            res[blockIdx.x * kFfnWgRows + lane] = (uint16_t)f2bf(sres);
         }
+        return;
+    }
+    const uint32_t tag = g0 + 1u;
+    if (lane < kFfnWgRows / 2)
+        publish64(&slots->d[blockIdx.x][lane], ((uint64_t)tag << 32) | dl[2 * lane] | (dl[2 * lane + 1] << 16));
+    if (lane == 0) {
+        float ss = 0.0f;  // in row order
+#pragma unroll
+        for (int i = 0; i < kFfnWgRows; ++i) ss = fmaf(bf2f(dl[i]), bf2f(dl[i]), ss);
+        publish64(&slots->part[blockIdx.x], ((uint64_t)tag << 32) | __float_as_uint(ss));
+    }
+    if (!leader) return;
+
+    // Leader: poll until every partial and the group's down outputs carry the tag.
+    constexpr int NP = (kFfnGrid + 63) / 64;
+    float part[NP];
+    uint32_t dq[4];
+    const bool mine_rows = lane < 2 * kFfnGroup;
+    const uint64_t t0 = wall_clock64();
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const bool real = lane + 64 * i < kFfnGrid;
+            const uint64_t v = collect64(&slots->part[min(lane + 64 * i, kFfnGrid - 1)]);
+            part[i] = real ? __uint_as_float((uint32_t)v) : 0.0f;
+            ok = ok && (!real || (uint32_t)(v >> 32) == tag);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint64_t v = collect64(&slots->d[lwg][(lane % 2) * 4 + k]);
+            dq[k] = (uint32_t)v;
+            ok = ok && (!mine_rows || (uint32_t)(v >> 32) == tag);
+        }
+        if (__all(ok)) break;
+        if (wall_clock64() - t0 > kSpinTicks) {
+            if (lane == 0) atomicOr(err, kErrSpinTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) tot += part[i];
+    const float inv = rms_inverse(wave_sum(tot), kH);
+    if (mine_rows) {
+        const uint32_t rw[4] = {r8.x, r8.y, r8.z, r8.w}, ww[4] = {w8.x, w8.y, w8.z, w8.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float d = bf2f((dq[k] >> (16 * h)) & 0xffffu);
+                const float n = rbf((d * inv) * bf2f((ww[k] >> (16 * h)) & 0xffffu));
+                float sres = rbf(bf2f((rw[k] >> (16 * h)) & 0xffffu) + n);
+                if (p.layer_scalar) sres = rbf(sres * lsv);
+                pair |= f2bf(sres) << (16 * h);
+            }
+            o[k] = pair;
+        }
+        *reinterpret_cast<uint4*>(res + lrow) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -1019,7 +1131,7 @@ static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevC
         hipError_t e;
         if (mm == 1 && ffn_fused_fits<F, SK>(ctx)) {
             ffn_fused_kernel<F, SK><<<dim3(kFfnGrid), dim3(kFfnBlock), 0, s>>>(
-                p, m0, ctx->pbuf, reinterpret_cast<float*>(ctx->dbuf), ctx->tickets, ctx->err);
+                p, m0, ctx->pbuf, reinterpret_cast<FfnSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
             continue;

@@ -28,6 +28,11 @@ constexpr int kTicketFfnBar = kTicketFfn + kTreeCounters * kMaxDecodeM;
 constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
 constexpr int kTicketCount = kTicketFfnGen + 1;
 
+// Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
+// never shared with another kernel).
+constexpr int kFfnPartSlots = 256;
+constexpr int kFfnSlotWords = kFfnPartSlots * 9;
+
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
 constexpr uint32_t kErrKvOffset = 2u;
@@ -42,6 +47,7 @@ struct DevCtx {
     uint16_t* pbuf = nullptr;     // [kMaxChunkM, 15360] bf16 (O: [M,3840]; FFN: GeGLU output)
     uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
+    uint64_t* ffn_part = nullptr; // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
     void* base = nullptr;
     int cus = 0;                  // compute units of the device
     int8_t ffn_fused[6] = {-1, -1, -1, -1, -1, -1};  // per (format, scale kind): grid fits resident? (-1 unknown)
