@@ -51,6 +51,8 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
+    const size_t t_opart = carve(sizeof(uint64_t) * kFfnSlotWords);
+    const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
     int cus = 0;
     *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (*err != hipSuccess) return nullptr;
@@ -73,6 +75,8 @@ DevCtx* device_context(hipError_t* err) {
     c.dbuf = reinterpret_cast<uint16_t*>(b + t_d);
     c.hbuf = reinterpret_cast<uint16_t*>(b + t_h);
     c.ffn_part = reinterpret_cast<uint64_t*>(b + t_part);
+    c.o_part = reinterpret_cast<uint64_t*>(b + t_opart);
+    c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
     c.base = base;
     return &c;
 }

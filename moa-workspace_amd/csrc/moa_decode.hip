@@ -105,6 +105,117 @@ __device__ __forceinline__ bool block_arrive_tree(uint32_t* tree, uint32_t nbloc
     return s_last;
 }
 
+// Tagged hand-off (single-launch kernels). A 64-bit word carries a value in its low half and the
+// launch's tag in its high half, written by one agent-scope store: a reader that sees the tag has
+// the whole value, so no counter has to follow the data. Tags come from monotonic counters (a
+// launch's epoch), so words left by an earlier launch never carry the current tag.
+constexpr uint64_t kSpinTicks = 1ull << 24;  // bound of every poll: ~168 ms of the 100 MHz wall clock
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+__device__ __forceinline__ void publish32(void* p, uint32_t v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t collect64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
+
+// Post-norm hand-off of the single-launch O and FFN kernels (240 workgroups of 16 output rows):
+// per workgroup one partial sum of squares (f32 bits) and eight words of two bf16 outputs.
+struct PostSlots {
+    uint64_t part[kFfnPartSlots];
+    uint64_t d[kFfnPartSlots][8];
+};
+static_assert(sizeof(PostSlots) == sizeof(uint64_t) * kFfnSlotWords, "slot area size");
+constexpr int kPostGrid = 240;     // workgroups of a post-norm hand-off
+constexpr int kPostWgRows = 16;    // output rows per workgroup
+constexpr int kPostLeaders = 8;    // leader workgroups
+constexpr int kPostGroup = kPostGrid / kPostLeaders;  // 30 workgroups per leader
+static_assert(kPostGrid * kPostWgRows == kH && 2 * kPostGroup <= 64, "a leader lane owns 8 outputs");
+
+// One wave of every workgroup b: publish its 16 outputs (bf16 bits dl[0..16)) and its partial sum
+// of squares (in row order).
+__device__ __forceinline__ void post_publish(PostSlots* slots, uint32_t tag, const uint32_t* dl, int lane) {
+    const int b = blockIdx.x;
+    if (lane < kPostWgRows / 2) publish64(&slots->d[b][lane], tagged(tag, dl[2 * lane] | (dl[2 * lane + 1] << 16)));
+    if (lane == 0) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPostWgRows; ++i) ss = fmaf(bf2f(dl[i]), bf2f(dl[i]), ss);
+        publish64(&slots->part[b], tagged(tag, __float_as_uint(ss)));
+    }
+}
+
+// Rows owned by lane l of leader g: 8 outputs of workgroup g + 8 (l / 2), from row (l % 2) * 8.
+__device__ __forceinline__ int post_leader_row(int lane) {
+    return (blockIdx.x + kPostLeaders * min(lane / 2, kPostGroup - 1)) * kPostWgRows + (lane % 2) * 8;
+}
+
+// One wave of leader workgroup g < kPostLeaders: poll until all 240 partial sums and the outputs of
+// workgroups g, g + 8, ... carry `tag`; sum the partials in a fixed order (the same bits in every
+// leader) and write those workgroups' residual rows in place:
+//   out = bf16(bf16(r + bf16(bf16(d * inv) * w)) * ls)    (ls skipped when has_ls is false)
+// FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241. r8 / w8: the lane's residual and
+// norm-weight values (prefetched by the caller at post_leader_row).
+__device__ __forceinline__ void post_leader(PostSlots* slots, uint32_t tag, uint16_t* res, const uint4& r8,
+                                            const uint4& w8, bool has_ls, float lsv, int lane, uint32_t* err) {
+    constexpr int NP = (kPostGrid + 63) / 64;
+    float part[NP];
+    uint32_t dq[4];
+    const bool mine_rows = lane < 2 * kPostGroup;
+    const int lwg = blockIdx.x + kPostLeaders * min(lane / 2, kPostGroup - 1);
+    const uint64_t t0 = wall_clock64();
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const bool real = lane + 64 * i < kPostGrid;
+            const uint64_t v = collect64(&slots->part[min(lane + 64 * i, kPostGrid - 1)]);
+            part[i] = real ? __uint_as_float((uint32_t)v) : 0.0f;
+            ok = ok && (!real || (uint32_t)(v >> 32) == tag);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint64_t v = collect64(&slots->d[lwg][(lane % 2) * 4 + k]);
+            dq[k] = (uint32_t)v;
+            ok = ok && (!mine_rows || (uint32_t)(v >> 32) == tag);
+        }
+        if (__all(ok)) break;
+        if (wall_clock64() - t0 > kSpinTicks) {
+            if (lane == 0) atomicOr(err, kErrSpinTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) tot += part[i];
+    const float inv = rms_inverse(wave_sum(tot), kH);
+    if (mine_rows) {
+        const uint32_t rw[4] = {r8.x, r8.y, r8.z, r8.w}, ww[4] = {w8.x, w8.y, w8.z, w8.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float d = bf2f((dq[k] >> (16 * h)) & 0xffffu);
+                const float n = rbf((d * inv) * bf2f((ww[k] >> (16 * h)) & 0xffffu));
+                float sres = rbf(bf2f((rw[k] >> (16 * h)) & 0xffffu) + n);
+                if (has_ls) sres = rbf(sres * lsv);
+                pair |= f2bf(sres) << (16 * h);
+            }
+            o[k] = pair;
+        }
+        *reinterpret_cast<uint4*>(res + post_leader_row(lane)) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 // Deterministic block sum (wave butterflies, then the four wave totals in order).
 __device__ __forceinline__ float block_sum(float v, float* red) {
     v = wave_sum(v);
@@ -168,6 +279,85 @@ __device__ __forceinline__ void rms_finish(const RmsStage& s, bool weighted, flo
     __syncthreads();
 }
 
+// Whole block of NW waves: h = RMSNorm(x, w) from an RmsStage into LDS as bf16.
+template <int NW>
+__device__ __forceinline__ void rms_finish_bf16(const RmsStage& s, uint16_t* __restrict__ lds, float* __restrict__ red) {
+    const int t = threadIdx.x;
+    const bool act = t < kH / 16;
+    float xv[16];
+    float ss = 0.0f;
+    bf16x8_to_f32(s.x0, xv);
+    bf16x8_to_f32(s.x1, xv + 8);
+    if (act) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);  // x*x is exact in f32
+    }
+    ss = wave_sum(ss);
+    if (lane_id() == 0) red[wave_id()] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += red[w];
+    const float inv = rms_inverse(tot, kH);
+    if (act) {
+        float wv[16];
+        bf16x8_to_f32(s.w0, wv);
+        bf16x8_to_f32(s.w1, wv + 8);
+        uint32_t h[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(lds + t * 16) = make_uint4(h[0], h[1], h[2], h[3]);
+        *reinterpret_cast<uint4*>(lds + t * 16 + 8) = make_uint4(h[4], h[5], h[6], h[7]);
+    }
+    __syncthreads();
+}
+
+// One wave: h = RMSNorm(x, w) over kH elements into LDS as bf16 -- 480 chunks of 8, lane l owning
+// chunks l + 64 i (i < 8; lanes 32-63 own 7). No workgroup barrier: the wave alone reduces, so the
+// other waves stay free to issue their weight loads. *_issue() loads the row (before any weight
+// load of the workgroup), *_finish() writes LDS once it has arrived.
+struct WaveRms {
+    static constexpr int N = (kH / 8 + 63) / 64;  // 8
+    uint4 x[N], w[N];
+};
+__device__ __forceinline__ void wave_rms_issue(WaveRms& s, const uint16_t* __restrict__ x,
+                                               const uint16_t* __restrict__ w, int lane) {
+#pragma unroll
+    for (int i = 0; i < WaveRms::N; ++i) {
+        const int c = min(lane + 64 * i, kH / 8 - 1);  // clamped: lanes past the row reload its last chunk
+        s.x[i] = ld16(x + c * 8);
+        s.w[i] = ld16(w + c * 8);
+    }
+}
+__device__ __forceinline__ void wave_rms_finish(const WaveRms& s, uint16_t* __restrict__ lds, int lane) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WaveRms::N; ++i) {
+        if (lane + 64 * i < kH / 8) {
+            float v[8];
+            bf16x8_to_f32(s.x[i], v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);  // x*x is exact in f32
+        }
+    }
+    const float inv = rms_inverse(wave_sum(ss), kH);
+#pragma unroll
+    for (int i = 0; i < WaveRms::N; ++i) {
+        const int c = lane + 64 * i;
+        if (c < kH / 8) {
+            float v[8], wv[8];
+            bf16x8_to_f32(s.x[i], v);
+            bf16x8_to_f32(s.w[i], wv);
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                h[e] = f2bf((v[2 * e] * inv) * wv[2 * e]) | (f2bf((v[2 * e + 1] * inv) * wv[2 * e + 1]) << 16);
+            *reinterpret_cast<uint4*>(lds + c * 8) = make_uint4(h[0], h[1], h[2], h[3]);
+        }
+    }
+}
+
 // A bf16 row of NC 8-element chunks, thread t owning chunks t + 256 i.
 template <int NC>
 struct RowStage {
@@ -206,6 +396,16 @@ __device__ __forceinline__ void lds_read(const float* lds, int at, float* out) {
     for (int i = 0; i < N; i += 4) {
         f32x4 v = *reinterpret_cast<const f32x4*>(lds + at + i);
         out[i] = v[0]; out[i + 1] = v[1]; out[i + 2] = v[2]; out[i + 3] = v[3];
+    }
+}
+
+// N bf16 activations at element `at` of an LDS row (16-byte aligned), as N/2 pairs.
+template <int N>
+__device__ __forceinline__ void lds_pairs(const uint16_t* lds, int at, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+        const uint4 v = *reinterpret_cast<const uint4*>(lds + at + 8 * i);
+        out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
     }
 }
 
@@ -451,6 +651,176 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
     qkv_head_epilogue(p, raw, head, m0 + m, err);
 }
 
+// ------------------------------------------------------------ QKV: single launch (one token row)
+// 256 workgroups of nine waves: eight compute four rows each and the ninth (the control wave)
+// normalises the activation row and finishes the head. Workgroup b computes 32 rows of head
+// h = b / 8 -- rows 16q .. 16q+15 and 128+16q .. 128+16q+15 of the head for q = b % 8, so every
+// row's RoPE partner (t ^ 128) is in the same workgroup. The head's RMSNorm needs the sum of
+// squares of all 256 rows: each workgroup publishes its partial sum tagged with the launch's
+// epoch (the head's epoch counter gets one add per workgroup at entry; the count read, divided
+// by 8, is the number of earlier launches) and polls the head's 8 tagged words. Then the
+// control wave normalises, rotates and stores the workgroup's 32 values.
+constexpr int kQkvWaves = 8;                                // row waves; wave 8 is the control wave
+constexpr int kQkvBlock = 64 * (kQkvWaves + 1);
+constexpr int kQkvRowsW = 4;                                // rows per row wave
+constexpr int kQkvWgRows = kQkvWaves * kQkvRowsW;           // 32
+constexpr int kQkvGrid = kQkvRows / kQkvWgRows;             // 256
+constexpr int kQkvPerHead = kDs / kQkvWgRows;               // 8 workgroups per head
+static_assert(kQkvPerHead * kQkvWgRows == kDs && kQkvGrid == 32 * kQkvPerHead, "QKV grid");
+static_assert(32 * kQkvPerHead == kQkvSlotWords, "one tagged word per workgroup");
+
+// Head-local row of slot s = 4 w + r (w < 4: first half of the head, w >= 4: second half).
+__device__ __forceinline__ int qkv_local_row(int q, int s) { return s < 16 ? 16 * q + s : 128 + 16 * q + (s - 16); }
+
+template <ScaleKind SK>
+__global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m0, uint64_t* slots, uint32_t* tickets,
+                                                              uint32_t* err) {
+    __shared__ uint16_t hs[kH];
+    __shared__ float raw[kQkvWgRows];
+    const int lane = lane_id(), wave = wave_id();
+    const bool ctl = wave == kQkvWaves;
+    const int head = blockIdx.x / kQkvPerHead, q = blockIdx.x % kQkvPerHead;
+
+    // the wave's four consecutive rows (the control wave's are never loaded)
+    const int t0 = qkv_local_row(q, min(wave, kQkvWaves - 1) * kQkvRowsW);
+    const uint8_t* W;
+    const void* S;
+    if (head < 16) { W = p.qw; S = p.qs; }
+    else if (head < 24) { W = p.kw; S = p.ks; }
+    else { W = p.vw; S = p.vs; }
+    const int mrow0 = (head < 16 ? head : (head < 24 ? head - 16 : head - 24)) * kDs + t0;  // row in its matrix
+    const float scale = load_scale<SK>(S, mrow0 + min(lane, kQkvRowsW - 1));
+
+    // Control wave: offsets and norm weight at entry (ahead of every weight load, so waiting for
+    // them later costs nothing); lane i < 32 serves head-local row qkv_local_row(q, i).
+    uint32_t ep = 0;
+    float wv = 1.0f, cv = 0.0f, sv = 0.0f;
+    int32_t rope_off = 0, kv_off = 0;
+    const int te = qkv_local_row(q, min(lane, kQkvWgRows - 1));
+    if (ctl) {
+        rope_off = *p.rope_off;
+        kv_off = *p.kv_off;
+        const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
+        if (wn) wv = bf2f(wn[te]);
+    }
+
+    // The control wave loads the activation row and normalises it alone; a barrier keeps every
+    // row wave's weight loads behind that row (a CU serves its loads in order). The row waves then
+    // issue all four rows at once.
+    WaveRms st;
+    if (ctl) wave_rms_issue(st, p.x + (size_t)m0 * kH, p.in_rms, lane);
+    __syncthreads();
+    constexpr int KI = 4;  // 3840 = 3.75 x 1024: lanes >= 48 idle in the last chunk
+    uint4 wq[kQkvRowsW][KI];
+    auto issue_row = [&](int r) {
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int col = j * 1024 + lane * 16;
+            const uint4 v = ld_stream(W + (size_t)(mrow0 + r) * kH + (col < kH ? col : 0));
+            wq[r][j] = col < kH ? v : make_uint4(0, 0, 0, 0);
+        }
+    };
+    // Three rows before the norm's barrier, one behind the first dots: a wave's issue stalls while
+    // its CU's load queue is full, and a wave stuck issuing would hold the barrier.
+    if (!ctl) {
+        issue_row(0);
+        issue_row(1);
+        issue_row(2);
+    } else {
+        wave_rms_finish(st, hs, lane);
+    }
+    __syncthreads();  // hs complete
+
+    // The epoch and the RoPE row behind the weights: they are needed only after the head's
+    // exchange, and loads retire in order -- issued first, the epoch add's return would hold up
+    // every later wait of the wave.
+    if (ctl) {
+        if (lane == 0) ep = counter_add(tickets + (kTicketQkvEpoch + head) * kTicketStride) / kQkvPerHead;
+        const int trow = rope_off / (kDs * 2) + m0;
+        if (head < 24 && rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && trow < kE) {
+            cv = bf2f(p.cos[(size_t)trow * kDs + te]);
+            sv = bf2f(p.sin[(size_t)trow * kDs + te]);
+        }
+    }
+
+    if (!ctl) {
+        uint32_t x[KI][8];
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const int col = j * 1024 + lane * 16;
+            if (col < kH) lds_pairs<16>(hs, col, x[j]);
+            else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[j][i] = 0u;
+            }
+        }
+        float mine = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kQkvRowsW; ++r) {
+            if (r + 3 < kQkvRowsW) issue_row(r + 3);
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KI; ++j) acc = dot_fp8x16_bf16(x[j], wq[r][j], acc);
+            acc = wave_sum(acc);
+            if (lane == r) mine = acc;
+        }
+        if (lane < kQkvRowsW) raw[wave * kQkvRowsW + lane] = rbf(mine * scale);  // generate_references.py:265-274
+    }
+    __syncthreads();
+    if (!ctl) return;
+
+    // RMSNorm over the head (sliding/rmsnorm.rs:22-153): partial sum of this workgroup's 32 rows,
+    // then the head's 8 partials in workgroup order.
+    const uint32_t tag = __shfl(ep, 0, kWave) + 1u;
+    uint64_t* hslots = slots + head * kQkvPerHead;
+    if (lane == 0) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kQkvWgRows; ++i) ss = fmaf(raw[i], raw[i], ss);  // exact squares of bf16
+        publish64(hslots + q, tagged(tag, __float_as_uint(ss)));
+    }
+    float part = 0.0f;
+    const uint64_t tp = wall_clock64();
+    for (;;) {
+        const uint64_t v = collect64(hslots + min(lane, kQkvPerHead - 1));
+        part = __uint_as_float((uint32_t)v);
+        if (__all(lane >= kQkvPerHead || (uint32_t)(v >> 32) == tag)) break;
+        if (wall_clock64() - tp > kSpinTicks) {
+            if (lane == 0) atomicOr(err, kErrSpinTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kQkvPerHead; ++i) tot += __shfl(part, i, kWave);
+    const float inv = rms_inverse(tot, kDs);
+
+    const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + m0 < kE;
+    const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
+    if (!rope_ok || !kv_ok) {  // the call writes nothing (no q_out, K or V) on a bad offset
+        if (blockIdx.x == 0 && lane == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
+        return;
+    }
+    const int slot = (kv_off / (kNs * kDs * 2) + m0) % kTs;
+    float n = raw[min(lane, kQkvWgRows - 1)] * inv;
+    if (head < 24) n = n * wv;
+    n = rbf(n);
+    // y = bf16(bf16(x*cos) + bf16(x_swap*sin_dev)); the table's sin has its low half negated
+    // (generate_references.py:200-210), so x_swap is a plain half swap: slot i ^ 16 holds row t ^ 128.
+    const float partner = __shfl_xor(n, 16, kWave);
+    if (lane >= kQkvWgRows) return;
+    if (head >= 24) {
+        p.v_cache[(size_t)slot * (kNs * kDs) + (head - 24) * kDs + te] = (uint16_t)f2bf(n);
+        return;
+    }
+    const float a = rbf(n * cv);
+    const float b = rbf(partner * sv);
+    uint16_t* dst = head < 16 ? p.q_out + (size_t)m0 * kQs + head * kDs
+                              : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs;
+    dst[te] = (uint16_t)f2bf(a + b);
+}
+
 // ===================================================================== O
 // ops::sliding_attention_output (FO/src/ops.rs:130-146). 3840 rows, K = 4096. Two rows per
 // wave, 8 per workgroup, 480 workgroups per token row.
@@ -499,6 +869,82 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
     block_post_residual(pbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, nullptr);
 }
 
+// ------------------------------------------------------------ O: single launch (one token row)
+// kPostGrid workgroups of eight waves, two rows per wave (16 per workgroup). The attention row
+// (4096 bf16) is loaded first -- one 16-byte chunk per thread -- and a barrier keeps every wave's
+// weight loads behind it (a CU serves its loads in order); the wave's two rows (8 KB) then go out
+// at once. Outputs and partial sums of squares leave through the tagged post-norm hand-off; the
+// kPostLeaders leaders apply post-norm and residual. The tag is the launch's epoch: the control
+// wave of workgroup b adds one to epoch counter b % 16 at entry (15 workgroups per counter), and
+// the count it reads, divided by 15, is the number of earlier launches.
+constexpr int kOWaves = 8;
+constexpr int kOBlock = 64 * kOWaves;
+constexpr int kORowsW = 2;  // rows per wave
+constexpr int kOEpochCounters = 16;
+static_assert(kPostGrid * kPostWgRows == kH && kOWaves * kORowsW == kPostWgRows, "O grid");
+static_assert(kPostGrid % kOEpochCounters == 0, "equal workgroups per epoch counter");
+
+template <ScaleKind SK>
+__global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, PostSlots* slots, uint32_t* tickets,
+                                                          uint32_t* err) {
+    __shared__ uint16_t xs[kQs];
+    __shared__ uint32_t dl[kPostWgRows];
+    const int lane = lane_id(), wave = wave_id();
+    const bool ctl = wave == kOWaves - 1;
+    const bool leader = blockIdx.x < kPostLeaders;
+    uint16_t* res = p.residual + (size_t)m0 * kH;
+
+    uint32_t ep = 0;
+    uint4 r8 = make_uint4(0, 0, 0, 0), w8 = make_uint4(0, 0, 0, 0);
+    if (ctl) {
+        if (leader) {
+            r8 = ld16(res + post_leader_row(lane));
+            w8 = ld16(p.post_rms + post_leader_row(lane));
+        }
+    }
+    const int row0 = blockIdx.x * kPostWgRows + wave * kORowsW;
+    const float scale = load_scale<SK>(p.os, row0 + min(lane, kORowsW - 1));
+    const uint4 xq = ld16(p.x + (size_t)m0 * kQs + threadIdx.x * 8);  // 512 chunks of 8
+    __syncthreads();
+    constexpr int KI = kQs / 1024;
+    uint4 wq[kORowsW][KI];
+#pragma unroll
+    for (int r = 0; r < kORowsW; ++r)
+#pragma unroll
+        for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * kQs + j * 1024 + lane * 16);
+    // the epoch add behind the weights (loads retire in order: issued first, its return would
+    // hold up every later wait of the wave)
+    if (ctl && lane == 0)
+        ep = counter_add(tickets + (kTicketOEpoch + blockIdx.x % kOEpochCounters) * kTicketStride) /
+             (kPostGrid / kOEpochCounters);
+    *reinterpret_cast<uint4*>(xs + threadIdx.x * 8) = xq;
+    __syncthreads();
+
+    float acc[kORowsW];
+#pragma unroll
+    for (int r = 0; r < kORowsW; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        uint32_t x[8];
+        lds_pairs<16>(xs, j * 1024 + lane * 16, x);
+#pragma unroll
+        for (int r = 0; r < kORowsW; ++r) acc[r] = dot_fp8x16_bf16(x, wq[r][j], acc[r]);
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kORowsW; ++r) {
+        const float d = wave_sum(acc[r]);
+        if (lane == r) mine = d;
+    }
+    if (lane < kORowsW) dl[wave * kORowsW + lane] = f2bf(mine * scale);  // generate_references.py:265-274
+    __syncthreads();
+    if (!ctl) return;
+    const uint32_t tag = __shfl(ep, 0, kWave) + 1u;
+    post_publish(slots, tag, dl, lane);
+    if (!leader) return;
+    post_leader(slots, tag, res, r8, w8, false, 1.0f, lane, err);
+}
+
 // =================================================================== FFN
 // ops::decoder_feedforward (FO/src/ops.rs:201-239). Two halves:
 //   up_gate: pre-RMSNorm, up and gate rows, GeGLU -> p[15360] (bf16)
@@ -545,49 +991,6 @@ __device__ __forceinline__ float chunk_dot2(const uint32_t* x, const Chunk<F>& c
     }
 }
 
-// N bf16 activations at element `at` of an LDS row (16-byte aligned), as N/2 pairs.
-template <int N>
-__device__ __forceinline__ void lds_pairs(const uint16_t* lds, int at, uint32_t* out) {
-#pragma unroll
-    for (int i = 0; i < N / 8; ++i) {
-        const uint4 v = *reinterpret_cast<const uint4*>(lds + at + 8 * i);
-        out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
-    }
-}
-
-// Whole block of NW waves: h = RMSNorm(x, w) from an RmsStage into LDS as bf16.
-template <int NW>
-__device__ __forceinline__ void rms_finish_bf16(const RmsStage& s, uint16_t* __restrict__ lds, float* __restrict__ red) {
-    const int t = threadIdx.x;
-    const bool act = t < kH / 16;
-    float xv[16];
-    float ss = 0.0f;
-    bf16x8_to_f32(s.x0, xv);
-    bf16x8_to_f32(s.x1, xv + 8);
-    if (act) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);  // x*x is exact in f32
-    }
-    ss = wave_sum(ss);
-    if (lane_id() == 0) red[wave_id()] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) tot += red[w];
-    const float inv = rms_inverse(tot, kH);
-    if (act) {
-        float wv[16];
-        bf16x8_to_f32(s.w0, wv);
-        bf16x8_to_f32(s.w1, wv + 8);
-        uint32_t h[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
-        *reinterpret_cast<uint4*>(lds + t * 16) = make_uint4(h[0], h[1], h[2], h[3]);
-        *reinterpret_cast<uint4*>(lds + t * 16 + 8) = make_uint4(h[4], h[5], h[6], h[7]);
-    }
-    __syncthreads();
-}
 
 // Pre-RMSNorm of the residual row x into hs (whole block of NW waves), then the wave's kUgRL
 // up/gate row pairs -- L-rows lbase + g*lstride, g < kUgRL -- through a D-deep ring of loads:
@@ -787,9 +1190,9 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
 //
 // Post-norm: every workgroup publishes its 16 down outputs and its partial sum of squares, each
 // 64-bit word tagged with g0 + 1 (a word holding the tag is complete, so no counters), and is
-// done. The kFfnLeaders leader workgroups poll the tags: leader g sums all 240 partials in a fixed
+// done. The kPostLeaders leader workgroups poll the tags: leader g sums all 240 partials in a fixed
 // order (deterministic, the same bits in every leader) and writes the outputs of the workgroups
-// b = g (mod kFfnLeaders). Few pollers keep the tagged lines free of contention.
+// b = g (mod kPostLeaders). Few pollers keep the tagged lines free of contention.
 //
 // Every poll is bounded by the wall clock (kSpinTicks): on expiry it sets kErrSpinTimeout in the
 // device error word and carries on, so every wave exits even if the grid were not resident.
@@ -800,25 +1203,8 @@ constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgrou
 constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
 constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
 constexpr int kFfnDownPre = 6;                      // down chunks per row loaded before the first barrier
-constexpr int kFfnLeaders = 8;                      // workgroups that finish the post-norm
-constexpr int kFfnGroup = kFfnGrid / kFfnLeaders;   // 30 workgroups per leader
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
-static_assert(kFfnGroup * kFfnLeaders == kFfnGrid && 2 * kFfnGroup <= 64, "a leader lane owns 8 outputs");
-static_assert(kFfnGrid <= kFfnPartSlots, "one tagged partial slot per workgroup");
-constexpr uint64_t kSpinTicks = 1ull << 24;  // ~168 ms of the 100 MHz wall clock
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void glb_void;
-
-__device__ __forceinline__ void publish32(void* p, uint32_t v) {
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void publish64(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t collect64(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+static_assert(kFfnGrid == kPostGrid && kFfnWgRows == kPostWgRows, "post-norm hand-off shape");
 
 // One lane per workgroup, after its workgroup's results are published and complete: arrive on
 // `tree` (kTreeCounters counters kTicketStride apart) and wait until `gen` reads `target`.
@@ -845,16 +1231,10 @@ __device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint
     }
 }
 
-// Tagged hand-off area of the single-launch FFN: per workgroup one partial-sum word (f32 bits |
-// tag << 32) and eight down-output words (two bf16 outputs | tag << 32).
-struct FfnSlots {
-    uint64_t part[kFfnPartSlots];
-    uint64_t d[kFfnPartSlots][kFfnWgRows / 2];
-};
 
 template <FfnFormat F, ScaleKind SK>
 __global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, FfnSlots* slots, uint32_t* tickets, uint32_t* err) {
+void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, PostSlots* slots, uint32_t* tickets, uint32_t* err) {
     constexpr int KD = down_chunks<F>();
     constexpr int EPC = elems_per_chunk<F>();
     __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
@@ -863,7 +1243,7 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, FfnSlots* slots, uint
     __shared__ uint32_t dl[kFfnWgRows];  // the workgroup's down outputs (bf16 bits)
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
-    const bool leader = blockIdx.x < kFfnLeaders;
+    const bool leader = blockIdx.x < kPostLeaders;
     uint32_t* gen = tickets + kTicketFfnGen * kTicketStride;
     uint32_t g0 = 0;
     if (ctl) g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -874,17 +1254,15 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, FfnSlots* slots, uint
     const float dscale = row_scale<F, SK>(p.down_s, p.down_g, drow0 + min(lane, kFfnDownR - 1));
 
     // Epilogue operands of the control wave, fetched now (off the critical path). With a post-norm
-    // a leader's lane l < 2 * kFfnGroup owns 8 outputs of workgroup g + 8 (l / 2), rows
+    // a leader's lane l < 2 * kPostGroup owns 8 outputs of workgroup g + 8 (l / 2), rows
     // (l % 2) * 8 ..; without one, every workgroup writes its own 16 outputs (lanes 0-15).
     uint4 r8 = make_uint4(0, 0, 0, 0), w8 = make_uint4(0, 0, 0, 0);
     uint32_t r1 = 0, ls_bits = 0;
-    const int lwg = blockIdx.x + kFfnLeaders * min(lane / 2, kFfnGroup - 1);  // leader: workgroup of lane
-    const int lrow = lwg * kFfnWgRows + (lane % 2) * 8;
     if (ctl) {
         if (p.layer_scalar) ls_bits = p.layer_scalar[0];
         if (post && leader) {
-            r8 = ld16(res + lrow);
-            w8 = ld16(p.post_rms + lrow);
+            r8 = ld16(res + post_leader_row(lane));
+            w8 = ld16(p.post_rms + post_leader_row(lane));
         } else if (!post) {
             r1 = res[blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1)];
         }
@@ -966,66 +1344,9 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, FfnSlots* slots, uint
         return;
     }
     const uint32_t tag = g0 + 1u;
-    if (lane < kFfnWgRows / 2)
-        publish64(&slots->d[blockIdx.x][lane], ((uint64_t)tag << 32) | dl[2 * lane] | (dl[2 * lane + 1] << 16));
-    if (lane == 0) {
-        float ss = 0.0f;  // in row order
-#pragma unroll
-        for (int i = 0; i < kFfnWgRows; ++i) ss = fmaf(bf2f(dl[i]), bf2f(dl[i]), ss);
-        publish64(&slots->part[blockIdx.x], ((uint64_t)tag << 32) | __float_as_uint(ss));
-    }
+    post_publish(slots, tag, dl, lane);
     if (!leader) return;
-
-    // Leader: poll until every partial and the group's down outputs carry the tag.
-    constexpr int NP = (kFfnGrid + 63) / 64;
-    float part[NP];
-    uint32_t dq[4];
-    const bool mine_rows = lane < 2 * kFfnGroup;
-    const uint64_t t0 = wall_clock64();
-    for (;;) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const bool real = lane + 64 * i < kFfnGrid;
-            const uint64_t v = collect64(&slots->part[min(lane + 64 * i, kFfnGrid - 1)]);
-            part[i] = real ? __uint_as_float((uint32_t)v) : 0.0f;
-            ok = ok && (!real || (uint32_t)(v >> 32) == tag);
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint64_t v = collect64(&slots->d[lwg][(lane % 2) * 4 + k]);
-            dq[k] = (uint32_t)v;
-            ok = ok && (!mine_rows || (uint32_t)(v >> 32) == tag);
-        }
-        if (__all(ok)) break;
-        if (wall_clock64() - t0 > kSpinTicks) {
-            if (lane == 0) atomicOr(err, kErrSpinTimeout);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) tot += part[i];
-    const float inv = rms_inverse(wave_sum(tot), kH);
-    if (mine_rows) {
-        const uint32_t rw[4] = {r8.x, r8.y, r8.z, r8.w}, ww[4] = {w8.x, w8.y, w8.z, w8.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t pair = 0;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const float d = bf2f((dq[k] >> (16 * h)) & 0xffffu);
-                const float n = rbf((d * inv) * bf2f((ww[k] >> (16 * h)) & 0xffffu));
-                float sres = rbf(bf2f((rw[k] >> (16 * h)) & 0xffffu) + n);
-                if (p.layer_scalar) sres = rbf(sres * lsv);
-                pair |= f2bf(sres) << (16 * h);
-            }
-            o[k] = pair;
-        }
-        *reinterpret_cast<uint4*>(res + lrow) = make_uint4(o[0], o[1], o[2], o[3]);
-    }
+    post_leader(slots, tag, res, r8, w8, p.layer_scalar != nullptr, lsv, lane, err);
 }
 
 // ========================================================== raw projection
@@ -1088,9 +1409,29 @@ hipError_t launch(K kernel, dim3 grid, hipStream_t s, A... args) {
 
 }  // namespace
 
+template <typename K>
+static bool fits_resident(int8_t& known, K kernel, int block, int grid, const DevCtx* ctx);
+
 hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx) {
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        if (mm == 1) {
+            const bool f32 = p.scale_kind == ScaleKind::F32;
+            if (f32 && fits_resident(ctx->qkv_fused[0], qkv_fused_kernel<ScaleKind::F32>, kQkvBlock, kQkvGrid, ctx)) {
+                qkv_fused_kernel<ScaleKind::F32><<<dim3(kQkvGrid), dim3(kQkvBlock), 0, s>>>(p, m0, ctx->qkv_part,
+                                                                                           ctx->tickets, ctx->err);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                continue;
+            }
+            if (!f32 && fits_resident(ctx->qkv_fused[1], qkv_fused_kernel<ScaleKind::BF16>, kQkvBlock, kQkvGrid, ctx)) {
+                qkv_fused_kernel<ScaleKind::BF16><<<dim3(kQkvGrid), dim3(kQkvBlock), 0, s>>>(p, m0, ctx->qkv_part,
+                                                                                            ctx->tickets, ctx->err);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                continue;
+            }
+        }
         const dim3 grid(kQkvRows / (4 * kQkvR), mm);
         hipError_t e = p.scale_kind == ScaleKind::F32
             ? launch(qkv_decode_kernel<ScaleKind::F32>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err)
@@ -1100,9 +1441,36 @@ hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* c
     return hipSuccess;
 }
 
+// Whether a single-launch kernel's grid of `grid` workgroups fits on the device at once.
+template <typename K>
+static bool fits_resident(int8_t& known, K kernel, int block, int grid, const DevCtx* ctx) {
+    if (known < 0) {
+        int per_cu = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0);
+        known = (e == hipSuccess && per_cu * ctx->cus >= grid) ? 1 : 0;
+    }
+    return known == 1;
+}
+
 hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx) {
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        if (mm == 1) {
+            const bool f32 = p.scale_kind == ScaleKind::F32;
+            PostSlots* slots = reinterpret_cast<PostSlots*>(ctx->o_part);
+            if (f32 && fits_resident(ctx->o_fused[0], o_fused_kernel<ScaleKind::F32>, kOBlock, kPostGrid, ctx)) {
+                o_fused_kernel<ScaleKind::F32><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets, ctx->err);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                continue;
+            }
+            if (!f32 && fits_resident(ctx->o_fused[1], o_fused_kernel<ScaleKind::BF16>, kOBlock, kPostGrid, ctx)) {
+                o_fused_kernel<ScaleKind::BF16><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets, ctx->err);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                continue;
+            }
+        }
         const dim3 grid(kH / (4 * kOR), mm);
         hipError_t e = p.scale_kind == ScaleKind::F32
             ? launch(o_decode_kernel<ScaleKind::F32>, grid, s, p, m0, ctx->pbuf, ctx->tickets)
@@ -1131,7 +1499,7 @@ static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevC
         hipError_t e;
         if (mm == 1 && ffn_fused_fits<F, SK>(ctx)) {
             ffn_fused_kernel<F, SK><<<dim3(kFfnGrid), dim3(kFfnBlock), 0, s>>>(
-                p, m0, ctx->pbuf, reinterpret_cast<FfnSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
+                p, m0, ctx->pbuf, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
             continue;

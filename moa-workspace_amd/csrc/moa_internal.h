@@ -26,12 +26,17 @@ constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
 constexpr int kTicketFfn = kTicketO + kTreeCounters * kMaxDecodeM;
 constexpr int kTicketFfnBar = kTicketFfn + kTreeCounters * kMaxDecodeM;
 constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
-constexpr int kTicketCount = kTicketFfnGen + 1;
+// Epoch counters of the single-launch O (16) and QKV (one per head) kernels: monotonic, never
+// reset; a workgroup adds one at entry and divides what it read by the workgroups per counter.
+constexpr int kTicketOEpoch = kTicketFfnGen + 1;
+constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
+constexpr int kTicketCount = kTicketQkvEpoch + 32;
 
 // Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
 // never shared with another kernel).
 constexpr int kFfnPartSlots = 256;
 constexpr int kFfnSlotWords = kFfnPartSlots * 9;
+constexpr int kQkvSlotWords = 32 * 8;
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
@@ -48,9 +53,13 @@ struct DevCtx {
     uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
     uint64_t* ffn_part = nullptr; // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
+    uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
+    uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
     void* base = nullptr;
     int cus = 0;                  // compute units of the device
     int8_t ffn_fused[6] = {-1, -1, -1, -1, -1, -1};  // per (format, scale kind): grid fits resident? (-1 unknown)
+    int8_t o_fused[2] = {-1, -1};                    // per scale kind
+    int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
