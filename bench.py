@@ -20,6 +20,11 @@ Prints one JSON line (stdout). `value` is microseconds per token for the step (l
 restatement of the reference's algorithm) on this host's cores for a bounded sample.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 10]
+    python bench.py --profile ffn|o|qkv [--steps 20]
+
+--profile runs one operator host-driven (one launch per call, no graph) over the rotating weight
+copies, then one device-to-device copy of 256 MiB: the fixed workload the rocprofv3 counter runs
+(FETCH_SIZE, WRITE_SIZE) use, the copy calibrating the counters against a known byte count.
 """
 from __future__ import annotations
 
@@ -53,6 +58,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
+    ap.add_argument("--profile", choices=("ffn", "o", "qkv"), default=None,
+                    help="run one operator host-driven for a counter profile, then a 256 MiB copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path is a per-GPU kernel; "
@@ -155,6 +162,19 @@ def main() -> int:
         torch.cuda.synchronize()
         return a.elapsed_time(b) / (reps * GRAPH_CALLS), reps * GRAPH_CALLS
 
+    if args.profile:
+        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv}[args.profile]
+        for i in range(args.steps):
+            fn(i)
+        torch.cuda.synchronize()
+        src = torch.empty(128 << 20, dtype=torch.int16, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"profile: {args.steps} x {args.profile}, then a copy of {src.numel() * 2} bytes")
+        assert ops.device_errors() == 0
+        return 0
+
     per_op = {}
     for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn)):
         ms, _ = graph_timed(fn, args.steps, args.warmup)
@@ -182,6 +202,12 @@ def main() -> int:
         cpu = cpu_baseline(ffn, o, qkv, args.cpu_seconds)
 
     f = per_op["ffn"]
+    # HBM bytes per FFN launch from the committed counter profile (FETCH_SIZE / WRITE_SIZE runs,
+    # calibrated against a copy of known size); null when the profile is absent.
+    traffic = None
+    tpath = ROOT / "profiles" / "hbm_traffic_m1.json"
+    if tpath.exists():
+        traffic = json.loads(tpath.read_text()).get("ffn_fused_kernel", {}).get("traffic_bytes")
     line = {
         "metric": METRIC, "value": round(ms_step * 1e3, 3), "unit": "us/token", "n_gpus": 1,
         "steps": steps_done, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
@@ -192,7 +218,8 @@ def main() -> int:
                    "hidden": 3840, "intermediate": 15360, "tokens_per_step": 1},
         "roofline": {"bound": "hbm", "kernel": "decoder_feedforward_fp8 (ffn_fused_kernel, one launch)",
                      "achieved": f["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": f["frac"],
-                     "algorithmic_bytes": BYTES["ffn"], "avg_us": f["us"], "traffic": None},
+                     "algorithmic_bytes": BYTES["ffn"], "avg_us": f["us"], "traffic": traffic,
+                     "traffic_source": "profiles/hbm_traffic_m1.md" if traffic else None},
         "ops": per_op,
         "us_per_token_host_driven": round(ms_step_host * 1e3, 3),
         "hbm_copy_GBps": round(copy_gbps, 1),

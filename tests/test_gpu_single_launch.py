@@ -1,0 +1,75 @@
+"""The single-launch kernels (one token row) and the per-row kernels beside them.
+
+A call of 17 rows runs a chunk of 16 rows through the per-row kernels and its last row through
+the single-launch kernel, so one call checks both paths against the oracle. Repeated calls
+interleaving different inputs check that no launch ever reads a tagged hand-off word left by an
+earlier launch (the tags are per-launch epochs): results must not depend on call history."""
+import numpy as np
+import pytest
+
+from gpu_util import gate, need_gpu, say
+from moa_amd import synth
+from test_gpu_ffn import FFN_ATOL, gpu_fp8, oracle_fp8
+from test_gpu_o import run_gpu as o_gpu
+from test_gpu_o import run_oracle as o_oracle
+from test_gpu_qkv import check_against_oracle
+from test_gpu_qkv import run_gpu as qkv_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def test_ffn_fp8_17_rows_both_paths():
+    need_gpu()
+    say("ffn fp8 M17 (16 per-row + 1 single-launch)")
+    d = synth.cfg_ffn_fp8(5, M=17)
+    gate(oracle_fp8(d), gpu_fp8(d), "ffn fp8 M17", atol=FFN_ATOL)
+
+
+def test_o_17_rows_both_paths():
+    need_gpu()
+    say("o M17 (16 per-row + 1 single-launch)")
+    d = synth.cfg_o(5, M=17)
+    gate(o_oracle(d), o_gpu(d), "o M17")
+
+
+def test_qkv_17_rows_both_paths():
+    need_gpu()
+    say("qkv M17 (16 per-row + 1 single-launch)")
+    d = synth.cfg_qkv(5, M=17, pos=1020)  # the ring wraps inside the call
+    check_against_oracle(d, "qkv M17", M=17)
+
+
+def test_o_results_do_not_depend_on_call_history():
+    need_gpu()
+    say("o: a, b, a")
+    a, b = synth.cfg_o(11), synth.cfg_o(12)
+    ra = o_gpu(a)
+    rb = o_gpu(b)
+    gate(o_oracle(a), ra, "o history a")
+    gate(o_oracle(b), rb, "o history b")
+    assert np.array_equal(ra, o_gpu(a)), "o: the same input gave different bits after another call"
+
+
+def test_ffn_results_do_not_depend_on_call_history():
+    need_gpu()
+    say("ffn: single-launch a, per-row b (M=2), single-launch a")
+    a, b = synth.cfg_ffn_fp8(6), synth.cfg_ffn_fp8(7, M=2)
+    ra = gpu_fp8(a)
+    rb = gpu_fp8(b)
+    gate(oracle_fp8(b), rb, "ffn history b", atol=FFN_ATOL)
+    assert np.array_equal(ra, gpu_fp8(a)), "ffn: the same input gave different bits after another call"
+    assert np.array_equal(ra, gpu_fp8(a, True, True))
+    gate(oracle_fp8(a), ra, "ffn history a", atol=FFN_ATOL)
+
+
+def test_qkv_results_do_not_depend_on_call_history():
+    need_gpu()
+    say("qkv: a, b, a")
+    a, b = synth.cfg_qkv(13), synth.cfg_qkv(14)
+    qa = qkv_gpu(a)
+    qb = qkv_gpu(b)
+    check_against_oracle(b, "qkv history b")
+    qa2 = qkv_gpu(a)
+    for x, y, name in zip(qa, qa2, ("q_out", "k_cache", "v_cache")):
+        assert np.array_equal(x, y), f"qkv: {name} differs for the same input after another call"
+    assert not np.array_equal(qa[0], qb[0])
