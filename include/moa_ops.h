@@ -41,6 +41,8 @@ extern "C" {
 
 #define MOA_DEVERR_ROPE_OFFSET 1u /* rope_offset not a multiple of 512 or past the table */
 #define MOA_DEVERR_KV_OFFSET 2u   /* kv_offset not a multiple of 4096 or past the ring */
+#define MOA_DEVERR_SPIN_TIMEOUT 4u /* a bounded cross-workgroup wait of a one-token call expired (the
+                                      call's results are unreliable; another process held the CUs) */
 
 /* Library version string. */
 const char* moa_version(void);

@@ -21,6 +21,7 @@ ERRORS = {
 }
 DEVERR_ROPE_OFFSET = 1
 DEVERR_KV_OFFSET = 2
+DEVERR_SPIN_TIMEOUT = 4
 
 
 class MoaError(RuntimeError):
