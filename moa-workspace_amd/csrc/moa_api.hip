@@ -50,6 +50,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);
     const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
+    const size_t t_f = carve(sizeof(float) * (size_t)kChunkSplitK * kMaxChunkM * kH);
     const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_opart = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
@@ -74,6 +75,7 @@ DevCtx* device_context(hipError_t* err) {
     c.pbuf = reinterpret_cast<uint16_t*>(b + t_p);
     c.dbuf = reinterpret_cast<uint16_t*>(b + t_d);
     c.hbuf = reinterpret_cast<uint16_t*>(b + t_h);
+    c.fbuf = reinterpret_cast<float*>(b + t_f);
     c.ffn_part = reinterpret_cast<uint64_t*>(b + t_part);
     c.o_part = reinterpret_cast<uint64_t*>(b + t_opart);
     c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
@@ -134,7 +136,14 @@ int qkv_common(const QkvParams& p, int M, void* stream) {
     int code = MOA_SUCCESS;
     DevCtx* ctx = ctx_or_fail(&code);
     if (!ctx) return code;
-    return finish(launch_qkv_decode(p, M, static_cast<hipStream_t>(stream), ctx), "sliding_project_qkv launch");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (M <= kMaxDecodeM) return finish(launch_qkv_decode(p, M, s, ctx), "sliding_project_qkv launch");
+    for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
+        const int e = finish(launch_qkv_chunk(p, m0, M - m0 < kMaxChunkM ? M - m0 : kMaxChunkM, s, ctx),
+                             "sliding_project_qkv launch");
+        if (e) return e;
+    }
+    return MOA_SUCCESS;
 }
 
 int o_common(const OParams& p, int M, void* stream) {
@@ -145,7 +154,14 @@ int o_common(const OParams& p, int M, void* stream) {
     int code = MOA_SUCCESS;
     DevCtx* ctx = ctx_or_fail(&code);
     if (!ctx) return code;
-    return finish(launch_o_decode(p, M, static_cast<hipStream_t>(stream), ctx), "sliding_attention_output launch");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (M <= kMaxDecodeM) return finish(launch_o_decode(p, M, s, ctx), "sliding_attention_output launch");
+    for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
+        const int e = finish(launch_o_chunk(p, m0, M - m0 < kMaxChunkM ? M - m0 : kMaxChunkM, s, ctx),
+                             "sliding_attention_output launch");
+        if (e) return e;
+    }
+    return MOA_SUCCESS;
 }
 
 int ffn_common(const FfnParams& p, int M, void* stream) {
@@ -170,7 +186,17 @@ int ffn_common(const FfnParams& p, int M, void* stream) {
     int code = MOA_SUCCESS;
     DevCtx* ctx = ctx_or_fail(&code);
     if (!ctx) return code;
-    return finish(launch_ffn_decode(p, M, static_cast<hipStream_t>(stream), ctx), "decoder_feedforward launch");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // More than kMaxDecodeM rows with FP8 weights take the MFMA path; FP4 formats stay on the
+    // per-row kernels (16 rows per launch).
+    if (M <= kMaxDecodeM || p.fmt != FfnFormat::FP8)
+        return finish(launch_ffn_decode(p, M, s, ctx), "decoder_feedforward launch");
+    for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
+        const int e = finish(launch_ffn_chunk(p, m0, M - m0 < kMaxChunkM ? M - m0 : kMaxChunkM, s, ctx),
+                             "decoder_feedforward launch");
+        if (e) return e;
+    }
+    return MOA_SUCCESS;
 }
 
 }  // namespace

@@ -12,6 +12,10 @@ namespace moa {
 constexpr int kMaxDecodeM = 16;
 // Rows handled by one call of the MFMA (M > kMaxDecodeM) path; larger calls are tiled by the host.
 constexpr int kMaxChunkM = 1024;
+// K splits of the MFMA path's 3840-wide projections (O, FFN down).
+constexpr int kChunkSplitK = 2;
+// QKV projection rows (Q | K | V).
+constexpr int kQkvRowsTotal = kQs + 2 * kPs;
 
 // Arrival counters. Each counter owns a 256-byte line: device-scope atomics to one line
 // serialise (~15 ns each), so counters never share a line and each kernel arrives once per
@@ -52,6 +56,7 @@ struct DevCtx {
     uint16_t* pbuf = nullptr;     // [kMaxChunkM, 15360] bf16 (O: [M,3840]; FFN: GeGLU output)
     uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
+    float* fbuf = nullptr;        // [kChunkSplitK, kMaxChunkM, 3840] f32 split-K partial sums (MFMA path)
     uint64_t* ffn_part = nullptr; // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
@@ -101,9 +106,10 @@ hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_decode(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s);
 
-hipError_t launch_qkv_chunk(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx);
-hipError_t launch_o_chunk(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
-hipError_t launch_ffn_chunk(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx);
+// MFMA path for one chunk of 1..kMaxChunkM token rows starting at row m0 of the call.
+hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);  // FP8 weights
 
 hipError_t launch_format_selftest(uint32_t* out, hipStream_t s);
 

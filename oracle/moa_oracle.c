@@ -203,20 +203,24 @@ void orc_rope_row(int head_dim, double theta, double factor, int pos, float* cos
 
 /* --------------------------------------------------------------- primitives */
 
-/* f32 dot with eight interleaved partial sums combined pairwise, the shape of a
- * vectorised BLAS reduction. The reference's own order (torch CPU) is unspecified,
- * so only the f32 accumulation width is part of the contract. */
+/* Sums of the reference's f32 accumulations: the reference adds in f32 in an unspecified
+ * order (torch CPU), so the oracle computes the value every order approximates, the exactly
+ * rounded f32 sum: eight interleaved f64 partial sums (each term -- a square of a bf16 value
+ * or a bf16 x fp8/fp4 product -- is exact in f64, and the sums of these few thousand terms
+ * are too), combined pairwise and rounded once to f32. Exact-dyadic known answers do not
+ * depend on this choice; on random inputs it keeps the oracle within one f32 rounding of the
+ * ideal, so a tolerance gate measures each implementation against the same anchor. */
 #define LANES 8
-static inline float reduce_lanes(float* acc) {
+static inline float reduce_lanes(double* acc) {
     for (int w = LANES / 2; w >= 1; w /= 2)
         for (int i = 0; i < w; ++i) acc[i] = acc[i] + acc[i + w];
-    return acc[0];
+    return (float)acc[0];
 }
 
 void orc_rmsnorm_row(const uint16_t* x, const uint16_t* w, int n, uint16_t* out) {
-    float acc[LANES] = {0};
+    double acc[LANES] = {0};
     for (int i = 0; i < n; ++i) {
-        float v = orc_bf16_to_f32(x[i]);
+        double v = orc_bf16_to_f32(x[i]);
         acc[i % LANES] += v * v;
     }
     float mean = reduce_lanes(acc) / (float)n;
@@ -251,8 +255,8 @@ static void init_luts(void) {
 }
 
 static inline float dot_fp8_row(const float* xf, const uint8_t* row, int K) {
-    float acc[LANES] = {0};
-    for (int k = 0; k < K; ++k) acc[k % LANES] += xf[k] * e4m3_lut[row[k]];
+    double acc[LANES] = {0};
+    for (int k = 0; k < K; ++k) acc[k % LANES] += (double)xf[k] * e4m3_lut[row[k]];
     return reduce_lanes(acc);
 }
 
@@ -348,7 +352,7 @@ static uint16_t ffn_proj_row(const orc_ffn_weights* w, int which, const float* x
     const uint8_t* mat = which == 0 ? w->up : which == 1 ? w->gate : w->down;
     const void* sc = which == 0 ? w->up_scale : which == 1 ? w->gate_scale : w->down_scale;
     float inv_g = which == 0 ? w->up_inv_global : which == 1 ? w->gate_inv_global : w->down_inv_global;
-    float acc[LANES] = {0};
+    double acc[LANES] = {0};
     if (w->format == ORC_FFN_FP8) {
         float d = dot_fp8_row(xf, mat + (size_t)n * K, K);
         return orc_bf16_rne(d * ((const float*)sc)[n]);
@@ -363,7 +367,7 @@ static uint16_t ffn_proj_row(const orc_ffn_weights* w, int which, const float* x
         float wv = w->format == ORC_FFN_NVFP4 ? e2m1_lut[nib] * e4m3_lut[srow[k / 16]]
                                                : e2m1_lut[nib] * e8m0_lut[srow[k / 32]];
         wv = orc_bf16_to_f32(orc_bf16_rne(wv));
-        acc[k % LANES] += xf[k] * wv;
+        acc[k % LANES] += (double)xf[k] * wv;
     }
     float d = reduce_lanes(acc);
     if (w->format == ORC_FFN_NVFP4) /* bf16 nn.Linear output, then GloballyScaled (:371-372) */
@@ -401,6 +405,7 @@ void orc_ffn_down(const uint16_t* p, const orc_ffn_weights* w, uint16_t* d, int 
 
 void orc_decoder_feedforward(uint16_t* residual, const uint16_t* pre_rms, const orc_ffn_weights* w,
                              const uint16_t* post_rms, const uint16_t* layer_scalar, int M) {
+    if (M <= 0) return;
     uint16_t* h = (uint16_t*)malloc(2 * (size_t)ORC_H * M);
     uint16_t* p = (uint16_t*)malloc(2 * (size_t)ORC_L * M);
     uint16_t* d = (uint16_t*)malloc(2 * (size_t)ORC_H * M);

@@ -1,13 +1,13 @@
-"""The single-launch kernels (one token row) and the per-row kernels beside them.
+"""The single-launch kernels (one token row) and the MFMA path of longer calls.
 
-A call of 17 rows runs a chunk of 16 rows through the per-row kernels and its last row through
-the single-launch kernel, so one call checks both paths against the oracle. Repeated calls
-interleaving different inputs check that no launch ever reads a tagged hand-off word left by an
-earlier launch (the tags are per-launch epochs): results must not depend on call history."""
+Calls of more than 16 rows take the MFMA path (FP8 weights): 17 rows (a partial row tile),
+64 (one full tile), 100 and 256 (BASELINE config 4's chunk length). Repeated calls interleaving
+different inputs check that no launch ever reads a tagged hand-off word left by an earlier launch
+(the tags are per-launch epochs): results must not depend on call history."""
 import numpy as np
 import pytest
 
-from gpu_util import gate, need_gpu, say
+from gpu_util import gate, gate_addend, need_gpu, say
 from moa_amd import synth
 from test_gpu_ffn import FFN_ATOL, gpu_fp8, oracle_fp8
 from test_gpu_o import run_gpu as o_gpu
@@ -18,25 +18,36 @@ from test_gpu_qkv import run_gpu as qkv_gpu
 pytestmark = pytest.mark.gpu
 
 
-def test_ffn_fp8_17_rows_both_paths():
+@pytest.mark.parametrize("M", [17, 64, 100, 256])
+def test_ffn_fp8_mfma_rows(M):
     need_gpu()
-    say("ffn fp8 M17 (16 per-row + 1 single-launch)")
-    d = synth.cfg_ffn_fp8(5, M=17)
-    gate(oracle_fp8(d), gpu_fp8(d), "ffn fp8 M17", atol=FFN_ATOL)
+    say(f"ffn fp8 M{M} (MFMA path)")
+    d = synth.cfg_ffn_fp8(5, M=M)
+    gate(oracle_fp8(d), gpu_fp8(d), f"ffn fp8 M{M}", atol=FFN_ATOL)
 
 
-def test_o_17_rows_both_paths():
+def test_ffn_fp8_mfma_rows_without_post_norm_and_scalar():
     need_gpu()
-    say("o M17 (16 per-row + 1 single-launch)")
-    d = synth.cfg_o(5, M=17)
-    gate(o_oracle(d), o_gpu(d), "o M17")
+    say("ffn fp8 M33 literal (MFMA path)")
+    d = synth.cfg_ffn_fp8(8, M=33)
+    gate_addend(oracle_fp8(d, False, False), gpu_fp8(d, False, False), d["residual"], "ffn fp8 M33 literal",
+                atol=FFN_ATOL)
 
 
-def test_qkv_17_rows_both_paths():
+@pytest.mark.parametrize("M", [17, 64, 100, 256])
+def test_o_mfma_rows(M):
     need_gpu()
-    say("qkv M17 (16 per-row + 1 single-launch)")
-    d = synth.cfg_qkv(5, M=17, pos=1020)  # the ring wraps inside the call
-    check_against_oracle(d, "qkv M17", M=17)
+    say(f"o M{M} (MFMA path)")
+    d = synth.cfg_o(5, M=M)
+    gate(o_oracle(d), o_gpu(d), f"o M{M}")
+
+
+@pytest.mark.parametrize("M", [17, 100, 256])
+def test_qkv_mfma_rows(M):
+    need_gpu()
+    say(f"qkv M{M} (MFMA path)")
+    d = synth.cfg_qkv(5, M=M, pos=1020)  # the ring wraps inside the call
+    check_against_oracle(d, f"qkv M{M}", M=M)
 
 
 def test_o_results_do_not_depend_on_call_history():
