@@ -46,6 +46,9 @@ MALL_BYTES = 256 << 20
 # Algorithmic bytes per call (weights + scales + operator-boundary vectors).
 BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848}
 GRAPH_CALLS = 40  # calls per captured graph
+# Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
+FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
 def log(*a):
@@ -58,8 +61,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
-    ap.add_argument("--profile", choices=("ffn", "o", "qkv"), default=None,
-                    help="run one operator host-driven for a counter profile, then a 256 MiB copy")
+    ap.add_argument("--chunk-rows", type=int, default=256,
+                    help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
+    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "chunk"), default=None,
+                    help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
+                         "then a 256 MiB copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path is a per-GPU kernel; "
@@ -105,6 +111,39 @@ def main() -> int:
     ro = torch.tensor([qkv["rope_offset"]], dtype=torch.int32, device="cuda")
     log(f"weight copies: ffn {nf}, o {no}, qkv {nq} "
         f"({(nf * BYTES['ffn'] + no * BYTES['o'] + nq * BYTES['qkv']) / 2**30:.2f} GiB)")
+
+    # Config 4: one decoder-layer chunk of CM prefill rows (positions 0..CM-1) through the MFMA path,
+    # on the same rotated FP8 weights; the O-projection's attention input is a seeded bf16 tensor.
+    CM = args.chunk_rows
+    if CM:
+        ck = synth.cfg_layer_chunk(0, M=CM)
+        c_x, c_attn = dev(ck["x"]), dev(ck["attn"])
+        c_res = c_x.clone()  # the layer's residual stream: O adds into it, the FFN updates it
+        c_cos, c_sin, c_kc, c_vc = (dev(ck[k]) for k in ("cos", "sin", "k_cache", "v_cache"))
+        c_q = torch.zeros(CM * 4096, dtype=torch.int16, device="cuda")
+        c_kv = torch.tensor([ck["kv_offset"]], dtype=torch.int32, device="cuda")
+        c_ro = torch.tensor([ck["rope_offset"]], dtype=torch.int32, device="cuda")
+
+    def run_cqkv(i):
+        w = QW[i % nq]
+        ops.sliding_project_qkv(c_x, w["q_weight"], w["k_weight"], w["v_weight"], w["q_weight_scale"],
+                                w["k_weight_scale"], w["v_weight_scale"], q["input_rms_weight"], q["q_rms_weight"],
+                                q["k_rms_weight"], c_kv, c_ro, c_cos, c_sin, c_kc, c_vc, c_q)
+
+    def run_co(i):
+        w = OW[i % no]
+        ops.sliding_attention_output(c_attn, o_post, w["o_weight"], w["o_weight_scale"], c_res)
+
+    def run_cffn(i):
+        w = FW[i % nf]
+        ops.decoder_feedforward_fp8(c_res, f_pre, w["up_weight"], w["gate_weight"], w["down_weight"],
+                                    w["up_weight_scale"], w["gate_weight_scale"], w["down_weight_scale"],
+                                    f_post, f_ls)
+
+    def run_layer(i):
+        run_cqkv(i)
+        run_co(i)
+        run_cffn(i)
 
     def run_ffn(i):
         w = FW[i % nf]
@@ -163,7 +202,7 @@ def main() -> int:
         return a.elapsed_time(b) / (reps * GRAPH_CALLS), reps * GRAPH_CALLS
 
     if args.profile:
-        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv}[args.profile]
+        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "chunk": run_layer}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -188,6 +227,19 @@ def main() -> int:
     ms_step, steps_done = graph_timed(run_step, args.steps, args.warmup)
     ms_step_host = timed(run_step, min(args.steps, 50), 5)
     log(f"step {ms_step * 1e3:9.2f} us/token   (host-driven {ms_step_host * 1e3:.2f} us)")
+
+    chunk = None
+    if CM:
+        chunk = {"rows": CM, "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "ops": {}}
+        for name, fn in (("qkv", run_cqkv), ("o", run_co), ("ffn", run_cffn), ("layer", run_layer)):
+            ms, _ = graph_timed(fn, GRAPH_CALLS, GRAPH_CALLS)
+            flops = CM * (sum(FLOPS_PER_ROW.values()) if name == "layer" else FLOPS_PER_ROW[name])
+            tf = flops / (ms * 1e-3) / 1e12
+            chunk["ops"][name] = {"us": round(ms * 1e3, 2), "us_per_token": round(ms * 1e3 / CM, 4),
+                                  "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                  "flops": flops}
+            log(f"chunk M={CM} {name:5} {ms * 1e3:9.2f} us  {tf:7.1f} TFLOP/s  "
+                f"{100 * tf / MFMA_BF16_PEAK_TFLOPS:5.1f}% of bf16 MFMA peak")
 
     # attainable HBM bandwidth: device-to-device copy of 2 GiB (read + write)
     big = torch.empty(1 << 30, dtype=torch.int16, device="cuda")
@@ -224,6 +276,7 @@ def main() -> int:
         "us_per_token_host_driven": round(ms_step_host * 1e3, 3),
         "hbm_copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": cpu,
+        "chunk": chunk,
     }
     print(json.dumps(line), flush=True)
     return 0

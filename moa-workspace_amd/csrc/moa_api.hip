@@ -50,7 +50,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);
     const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
-    const size_t t_f = carve(sizeof(float) * (size_t)kChunkSplitK * kMaxChunkM * kH);
+    const size_t t_f = carve(sizeof(float) * kChunkPartFloats);
     const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_opart = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);

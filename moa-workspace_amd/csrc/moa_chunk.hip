@@ -22,11 +22,12 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kCkBlock = 256;        // four waves, 2 (rows) x 2 (columns)
-constexpr int kCkBM = 64;            // rows per workgroup
-constexpr int kCkBN = 128;           // columns per workgroup (64 per wave: two 32-column MFMA blocks)
-constexpr int kCkBK = 64;            // k per pipeline step
-constexpr int kCkXStride = kCkBK + 8;  // LDS row stride (elements): padding spreads the rows over banks
+constexpr int kCkBlock = 256;          // four waves
+constexpr int kCkBM = 256;             // rows per workgroup: wave w takes rows 64 w .. 64 w + 63
+constexpr int kCkBN = 128;             // weight rows per workgroup (GeGLU: 64 up + the same 64 gate)
+constexpr int kCkBK = 64;              // k per pipeline step
+constexpr int kCkWStride = kCkBK + 16; // LDS bytes per staged weight row: 80 puts 16 rows on distinct banks
+constexpr int kCkTilesTarget = 264;    // split-K aims at about one workgroup per CU
 
 // 8 E4M3 codes (two dwords, lower index in the low byte) widened to 8 bf16.
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
@@ -39,160 +40,253 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
+// Activation layout of the MFMA path ("A tiles"): a row-major [M][K] bf16 matrix is stored as
+// 4 KB tiles of 32 rows x 64 k, ordered [row block][k step]. Inside a tile the 16-byte unit
+// (i, lane), at element 512 i + 8 lane, holds row lane % 32, k 32 (lane / 32) + 8 i .. + 7: what
+// lane `lane` feeds to the step's MFMA i. One 16-byte load per lane then reads 1 KB contiguous
+// (eight cache lines) instead of touching 32 rows. Rows are padded to a multiple of 32.
+__host__ __device__ __forceinline__ size_t atile_off(int m, int k, int K) {
+    const int kk = k & 63;
+    return ((size_t)(m >> 5) * (K >> 6) + (k >> 6)) * 2048 + ((kk >> 3) & 3) * 512 + ((m & 31) + 32 * (kk >> 5)) * 8 +
+           (k & 7);
+}
+
 template <ScaleKind SK>
 __device__ __forceinline__ float chunk_scale(const void* p, int i) {
     if constexpr (SK == ScaleKind::F32) return static_cast<const float*>(p)[i];
     else return bf2f(static_cast<const uint16_t*>(p)[i]);
 }
 
-enum class Epi { Bf16Scaled, F32Partial, GeGLU };
+enum class Epi { F32Partial, GeGLU };
 
 // The contraction of one chunk. Columns [nseg[i], nseg[i+1]) use weight matrix w[i] (rows
-// n - nseg[i]) and scales s[i]; a workgroup's 128 columns never straddle two matrices.
+// n - nseg[i]); a workgroup's 128 columns never straddle two matrices.
 struct GemmArgs {
-    const uint16_t* x;  // bf16 [M][ldx]
-    int ldx;
+    const uint16_t* x;  // bf16 A tiles of [M][K]
     int M, N, K;        // K: full reduction length; each of gridDim.z splits takes K / gridDim.z
     const uint8_t* w[3];
-    const void* s[3];
     int nseg[4];
     int nsegs;
-    const uint8_t* w2;  // GeGLU: the gate matrix (w[0] is up)
+    const uint8_t* w2;  // GeGLU: the gate matrix (w[0] is up); s[0], s2 their scales
+    const void* s0;
     const void* s2;
-    uint16_t* y;        // Bf16Scaled, GeGLU: bf16 [M][ldy]
-    int ldy;
+    uint16_t* y;        // GeGLU: bf16 A tiles of [M][N] (the down projection's input)
     float* yf;          // F32Partial: [gridDim.z][M][N]
 };
 
-// Workgroup (bx, by, bz): rows 64 by .. +64, columns 128 bx .. +128, k split bz. Wave w covers
-// rows 32 (w >> 1) .. +32 and columns 64 (w & 1) .. +64 (two 32 x 32 MFMA blocks). Per 64-k step
-// the workgroup stages the X tile in LDS (double-buffered); each wave loads its own weight rows
-// (16 bytes per lane per 32 k). Within a 32-k block the k order fed to the two MFMAs is
-// permuted identically for A and B (lane half h takes k 16h .. 16h+7 in the first MFMA and
-// 16h+8 .. 16h+15 in the second), so one 16-byte weight load feeds both.
+template <int V>
+struct Par {
+    static constexpr int value = V;
+};
+
+// Buffer resource over [base, base + bytes): loads past the end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ck_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+constexpr int kCkNt = 2;  // cache policy: non-temporal (weights are read once)
+
+// Workgroup (bx, by, bz): rows 256 by .. +256, a 128-row weight tile (columns 128 bx .. +128,
+// or for GeGLU up and gate rows 64 bx .. +64), k split bz. Wave w computes rows 64 w .. +64 of
+// the tile against all 128 weight rows: 2 x 4 blocks of v_mfma_f32_32x32x16_bf16, 128 f32
+// accumulators per lane.
+//   Activations (A tiles) go from memory straight into the registers of the lanes that feed them
+//   to the MFMA (no other wave needs them): per 64-k step lane (l32, h) holds 32 bf16 of row l32
+//   of each 32-row block, k 32 h .. 32 h + 31, in four 1 KB-contiguous loads. MFMA j (j = 0..3)
+//   of the step takes k 32 h + 8 j .. + 7 from lane half h, for A and B alike, which is a fixed
+//   permutation of the step's 64 k. Row blocks past M read zeros (the buffer ends there); rows
+//   past M are not stored.
+//   Weights (FP8) are staged once per workgroup through LDS: each thread moves two 16-byte chunks
+//   per step, loaded eight steps ahead (HBM latency at the rate the whole chip streams weights)
+//   and written two steps ahead; a wave reads
+//   32 bytes per lane per 32-column block and widens them to bf16 (exact for E4M3).
+//   All loads are buffer loads whose per-lane offsets are fixed: the step moves the scalar
+//   offset only. Prefetches past the last step repeat the last step (harmless), so the loop body
+//   has no branches.
 template <Epi E, ScaleKind SK>
-__global__ __launch_bounds__(kCkBlock) void chunk_gemm_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][kCkBM * kCkXStride];
+__global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_gemm_kernel(GemmArgs g) {
+    // three weight buffers during the loop; the GeGLU epilogue reuses the space for its transpose
+    constexpr int kWsBytes = kCkBN * kCkWStride, kTpStride = 72;
+    constexpr int kLds = 3 * kWsBytes > 4 * 64 * kTpStride * 2 ? 3 * kWsBytes : 4 * 64 * kTpStride * 2;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
+    uint8_t(*ws)[kWsBytes] = reinterpret_cast<uint8_t(*)[kWsBytes]>(smem);
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
     const int hf = lane >> 5, l32 = lane & 31;
-    const int mb0 = blockIdx.y * kCkBM;
-    const int n_wave = blockIdx.x * kCkBN + wn * 64;
+    const int m_blk = blockIdx.y * kCkBM;
+    const int m_wave = m_blk + wave * 64;
     const int kz = g.K / gridDim.z, kbeg = blockIdx.z * kz, nsteps = kz / kCkBK;
 
+    // staged weight rows of this thread: tile rows r0 and r0 + 64, 16 bytes at 16 q of each step
+    const int r0 = t >> 2, q = t & 3;
+    __amdgpu_buffer_rsrc_t wrs[2];
+    int wvo[2];
     int seg = 0;
-    while (seg + 1 < g.nsegs && blockIdx.x * kCkBN >= g.nseg[seg + 1]) ++seg;
-    const uint8_t* W = g.w[seg];
-    const uint8_t* wr[2];
-    const uint8_t* wr2[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const size_t row = (size_t)(n_wave - g.nseg[seg] + nb * 32 + l32);
-        wr[nb] = W + row * g.K + 16 * hf + kbeg;
-        wr2[nb] = E == Epi::GeGLU ? g.w2 + row * g.K + 16 * hf + kbeg : nullptr;
+    if constexpr (E == Epi::GeGLU) {
+        const size_t off = (size_t)blockIdx.x * 64 * g.K;
+        wrs[0] = ck_rsrc(g.w[0] + off, 64u * g.K);
+        wrs[1] = ck_rsrc(g.w2 + off, 64u * g.K);
+        wvo[0] = wvo[1] = r0 * g.K + kbeg + 16 * q;
+    } else {
+        const int n0 = blockIdx.x * kCkBN;
+        while (seg + 1 < g.nsegs && n0 >= g.nseg[seg + 1]) ++seg;
+        wrs[0] = wrs[1] = ck_rsrc(g.w[seg] + (size_t)(n0 - g.nseg[seg]) * g.K, (uint32_t)kCkBN * g.K);
+        wvo[0] = r0 * g.K + kbeg + 16 * q;
+        wvo[1] = (r0 + 64) * g.K + kbeg + 16 * q;
     }
-    // X staging: 64 rows x 64 k = 512 chunks of 8; thread t moves chunks t and t + 256
-    const uint16_t* xr[2];
-    bool xok[2];
-    int xoff[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = t + 256 * i, row = c >> 3, kc = (c & 7) * 8;
-        xok[i] = mb0 + row < g.M;
-        xr[i] = g.x + (size_t)min(mb0 + row, g.M - 1) * g.ldx + kbeg + kc;
-        xoff[i] = row * kCkXStride + kc;
-    }
+    const int wdst0 = r0 * kCkWStride + 16 * q, wdst1 = (r0 + 64) * kCkWStride + 16 * q;
 
-    f32x16 acc[2], acc2[2];
+    const int kst = g.K / kCkBK;  // 64-k steps (A tiles) per row block
+    const int rblks = (min(g.M - m_blk, kCkBM) + 31) >> 5;
+    const __amdgpu_buffer_rsrc_t ars = ck_rsrc(g.x + (size_t)(m_blk >> 5) * kst * 2048, (uint32_t)rblks * kst * 4096u);
+    int avo[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[nb][r] = acc2[nb][r] = 0.0f;
+    for (int mb = 0; mb < 2; ++mb) avo[mb] = ((wave * 2 + mb) * kst * 2048 + lane * 8) * 2 + (kbeg / kCkBK) * 4096;
 
-    uint4 wq[2][2], wq2[2][2];  // [n block][32-k block]
-    auto load_w = [&](int step, uint4 (&dst)[2][2], uint4 (&dst2)[2][2]) {
+    f32x16 acc[2][4];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                dst[nb][kb] = ld_stream(wr[nb] + step * kCkBK + kb * 32);
-                if constexpr (E == Epi::GeGLU) dst2[nb][kb] = ld_stream(wr2[nb] + step * kCkBK + kb * 32);
-            }
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
+
+    constexpr int WD = 6;  // weight register sets: W(s + 2) is loaded six steps before it is staged
+    uint4 wr[WD][2];       // [set][row pair]
+    uint4 ar[2][2][4];     // [set][32-row block][16 bytes]
+    uint4 braw[2][2];      // FP8 B fragments as read from LDS: [set][32 bytes]
+    bf16x8 bb[2][4];       // widened: [set][MFMA j]
+    const int last = nsteps - 1;
+    auto load_w = [&](uint4 (&dst)[2], int s) {
+        const int so = min(s, last) * kCkBK;
+        dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[0], wvo[0], so, kCkNt));
+        dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[1], wvo[1], so, kCkNt));
     };
-    uint4 xq[2];
-    auto load_x = [&](int step) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint4 v = ld16(xr[i] + step * kCkBK);
-            xq[i] = xok[i] ? v : make_uint4(0, 0, 0, 0);
-        }
+    auto store_w = [&](const uint4 (&src)[2], int buf) {
+        *reinterpret_cast<uint4*>(&ws[buf][wdst0]) = src[0];
+        *reinterpret_cast<uint4*>(&ws[buf][wdst1]) = src[1];
     };
-    auto store_x = [&](int buf) {
+    auto load_a = [&](uint4 (&dst)[2][4], int s) {
+        const int so = min(s, last) * 4096;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(&xs[buf][xoff[i]]) = xq[i];
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dst[mb][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ars, avo[mb] + 1024 * i, so, 0));
+    };
+    auto read_b = [&](uint4 (&dst)[2], int buf, int nb) {
+        const uint8_t* bp = &ws[buf][(32 * nb + l32) * kCkWStride + 32 * hf];
+        dst[0] = *reinterpret_cast<const uint4*>(bp);
+        dst[1] = *reinterpret_cast<const uint4*>(bp + 16);
+    };
+    auto widen = [&](bf16x8 (&dst)[4], const uint4 (&src)[2]) {
+        dst[0] = fp8x8_to_bf16(src[0].x, src[0].y);
+        dst[1] = fp8x8_to_bf16(src[0].z, src[0].w);
+        dst[2] = fp8x8_to_bf16(src[1].x, src[1].y);
+        dst[3] = fp8x8_to_bf16(src[1].z, src[1].w);
+    };
+    auto mfma8 = [&](const uint4 (&a)[2][4], const bf16x8 (&b)[4], auto NB) {
+        constexpr int nb = decltype(NB)::value;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[mb][j]), b[j], acc[mb][nb], 0, 0, 0);
     };
 
-    load_x(0);
-    load_w(0, wq, wq2);
-    store_x(0);
+    // Three LDS buffers: step s reads buffer s mod 3 and stages W(s + 2) into buffer (s + 2) mod 3
+    // (last read in step s - 1, before the barrier that opens step s), so the first fragment of
+    // step s + 1 (buffer (s + 1) mod 3, staged in step s - 1) is read before step s ends. Within a
+    // step, fragment nb + 1 is widened while fragment nb's eight MFMAs run.
+#pragma unroll
+    for (int i = 0; i < WD; ++i) load_w(wr[i], i);
+    load_a(ar[0], 0);
+    store_w(wr[0], 0);
+    store_w(wr[1], 1);
+    load_w(wr[0], WD);
+    load_w(wr[1], WD + 1);
     __syncthreads();
-    for (int s = 0; s < nsteps; ++s) {
-        const int cur = s & 1;
-        uint4 wn[2][2], wn2[2][2];
-        if (s + 1 < nsteps) {
-            load_x(s + 1);
-            load_w(s + 1, wn, wn2);
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const uint16_t* ap = &xs[cur][(wm * 32 + l32) * kCkXStride + kb * 32 + 16 * hf];
-            const bf16x8 a0 = as_bf16x8(*reinterpret_cast<const uint4*>(ap));
-            const bf16x8 a1 = as_bf16x8(*reinterpret_cast<const uint4*>(ap + 8));
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const uint4 q = wq[nb][kb];
-                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, fp8x8_to_bf16(q.x, q.y), acc[nb], 0, 0, 0);
-                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, fp8x8_to_bf16(q.z, q.w), acc[nb], 0, 0, 0);
-                if constexpr (E == Epi::GeGLU) {
-                    const uint4 q2 = wq2[nb][kb];
-                    acc2[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, fp8x8_to_bf16(q2.x, q2.y), acc2[nb], 0, 0, 0);
-                    acc2[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, fp8x8_to_bf16(q2.z, q2.w), acc2[nb], 0, 0, 0);
-                }
-            }
-        }
-        if (s + 1 < nsteps) {
-            store_x(cur ^ 1);
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    wq[nb][kb] = wn[nb][kb];
-                    if constexpr (E == Epi::GeGLU) wq2[nb][kb] = wn2[nb][kb];
-                }
-        }
+    read_b(braw[0], 0, 0);
+    auto body = [&](auto P, int s) {
+        constexpr int c = decltype(P)::value;  // s mod 6
+        constexpr int cb = c % 3, nbuf = (c + 1) % 3;
+        const uint4(&a)[2][4] = ar[c & 1];
+        load_a(ar[(c + 1) & 1], s + 1);
+        store_w(wr[(c + 2) % WD], (c + 2) % 3);
+        load_w(wr[(c + 2) % WD], s + 2 + WD);
+        __builtin_amdgcn_sched_barrier(0);
+        widen(bb[0], braw[0]);
+        read_b(braw[1], cb, 1);
+        mfma8(a, bb[0], Par<0>{});
+        widen(bb[1], braw[1]);
+        read_b(braw[0], cb, 2);
+        mfma8(a, bb[1], Par<1>{});
+        widen(bb[0], braw[0]);
+        read_b(braw[1], cb, 3);
+        mfma8(a, bb[0], Par<2>{});
+        widen(bb[1], braw[1]);
+        read_b(braw[0], nbuf, 0);
+        mfma8(a, bb[1], Par<3>{});
         __syncthreads();
+    };
+    int s = 0;
+    for (; s + 5 < nsteps; s += 6) {
+        body(Par<0>{}, s);
+        body(Par<1>{}, s + 1);
+        body(Par<2>{}, s + 2);
+        body(Par<3>{}, s + 3);
+        body(Par<4>{}, s + 4);
+        body(Par<5>{}, s + 5);
     }
+    if (s < nsteps) body(Par<0>{}, s++);
+    if (s < nsteps) body(Par<1>{}, s++);
+    if (s < nsteps) body(Par<2>{}, s++);
+    if (s < nsteps) body(Par<3>{}, s++);
+    if (s < nsteps) body(Par<4>{}, s++);
 
-    // Accumulator element r of lane l: row 8 (r / 4) + 4 (l / 32) + r % 4 of the wave's 32-row
-    // block, column l % 32 of the 32-column block.
+    if constexpr (E == Epi::GeGLU) __syncthreads();  // the loop's LDS reads are done: the transpose may reuse it
+    if (m_wave >= g.M) return;
+    // Accumulator element r of lane l: row 8 (r / 4) + 4 (l / 32) + r % 4 of the 32-row block,
+    // column l % 32 of the 32-column block. A wave whose 64 rows all lie below M stores without
+    // per-element tests (a test per element would serialise the 64-128 element computations).
+    const bool full = m_wave + 64 <= g.M;
+    if constexpr (E == Epi::F32Partial) {
+        float* yz = g.yf + (size_t)blockIdx.z * g.M * g.N + blockIdx.x * kCkBN + l32;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int n = n_wave + nb * 32 + l32;
-        float sc = 1.0f, sc2 = 1.0f;
-        if constexpr (E != Epi::F32Partial) sc = chunk_scale<SK>(g.s[seg], n - g.nseg[seg]);
-        if constexpr (E == Epi::GeGLU) sc2 = chunk_scale<SK>(g.s2, n);
+        for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = mb0 + wm * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-            if (m >= g.M) continue;
-            if constexpr (E == Epi::Bf16Scaled) {
-                g.y[(size_t)m * g.ldy + n] = (uint16_t)f2bf(acc[nb][r] * sc);  // generate_references.py:265-274
-            } else if constexpr (E == Epi::F32Partial) {
-                g.yf[((size_t)blockIdx.z * g.M + m) * g.N + n] = acc[nb][r];
-            } else {
-                const float up = rbf(acc[nb][r] * sc), gate = rbf(acc2[nb][r] * sc2);
-                g.y[(size_t)m * g.ldy + n] = (uint16_t)f2bf(rbf(gelu_tanh(gate)) * up);  // gemma4.py:197
-            }
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m_wave + 32 * mb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (full || m < g.M) yz[(size_t)m * g.N + nb * 32] = acc[mb][nb][r];
+                }
+    } else {
+        // p = bf16(gelu(gate) * up) for the wave's 64 rows x 64 columns, transposed through the
+        // wave's own 9 KB of LDS (row stride 72 elements) so that each lane then stores whole
+        // 16-byte units of the A tiles (row, 8 consecutive columns).
+        uint16_t* tp = reinterpret_cast<uint16_t*>(smem) + wave * (64 * kTpStride);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int n = blockIdx.x * 64 + nb * 32 + l32;
+            const float su = chunk_scale<SK>(g.s0, n), sg = chunk_scale<SK>(g.s2, n);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int ml = 32 * mb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    const float up = rbf(acc[mb][nb][r] * su), gate = rbf(acc[mb][nb + 2][r] * sg);
+                    tp[ml * kTpStride + nb * 32 + l32] = (uint16_t)f2bf(rbf(gelu_tanh(gate)) * up);  // gemma4.py:197
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        // 64 rows x 8 units of 16 bytes = 512 units; lane takes units lane + 64 i
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int u = lane + 64 * i, ml = u >> 3, cu = u & 7;
+            const int m = m_wave + ml;
+            const uint4 v = *reinterpret_cast<const uint4*>(&tp[ml * kTpStride + cu * 8]);
+            if (full || m < g.M) *reinterpret_cast<uint4*>(g.y + atile_off(m, blockIdx.x * 64 + cu * 8, g.N)) = v;
         }
     }
 }
@@ -206,8 +300,8 @@ __device__ __forceinline__ float ck_block_sum(float v, float* red) {
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) (gemma4.py:83-89). One workgroup per row;
-// thread t < 240 owns elements 16t .. 16t+15.
+// out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) (gemma4.py:83-89), written as A tiles.
+// One workgroup per row; thread t < 240 owns elements 16t .. 16t+15.
 __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint16_t* __restrict__ x,
                                                                       const uint16_t* __restrict__ w,
                                                                       uint16_t* __restrict__ out) {
@@ -232,16 +326,27 @@ __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
-    uint16_t* o = out + (size_t)m * kH + c * 16;
-    *reinterpret_cast<uint4*>(o) = make_uint4(h[0], h[1], h[2], h[3]);
-    *reinterpret_cast<uint4*>(o + 8) = make_uint4(h[4], h[5], h[6], h[7]);
+    *reinterpret_cast<uint4*>(out + atile_off(m, c * 16, kH)) = make_uint4(h[0], h[1], h[2], h[3]);
+    *reinterpret_cast<uint4*>(out + atile_off(m, c * 16 + 8, kH)) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
-// Per (head, row): RMSNorm over the head's 256 raw values (q, k weighted; v plain), RoPE on q
-// and k, and the q_out / ring-cache stores (sliding/rmsnorm.rs:22-153, rope.rs:9-211,
-// ops.rs:72-75). Thread t owns head element t; RoPE partners (t, t ^ 128) meet in LDS. A bad
-// offset writes nothing; workgroup (0, 0) reports it.
-__global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, int m0, const uint16_t* __restrict__ raw,
+// Row-major bf16 [M][K] -> A tiles (the O-projection's input arrives row-major). One workgroup
+// per row; thread t moves 16-byte units t, t + 256, ...
+__global__ __launch_bounds__(kCkBlock) void chunk_tile_rows_kernel(const uint16_t* __restrict__ x, int K,
+                                                                   uint16_t* __restrict__ out) {
+    const int m = blockIdx.x;
+    for (int u = threadIdx.x; u < K / 8; u += kCkBlock)
+        *reinterpret_cast<uint4*>(out + atile_off(m, u * 8, K)) = ld16(x + (size_t)m * K + u * 8);
+}
+
+// Per (head, row): raw = bf16((sum of the split-K partials) * s), RMSNorm over the head's 256 raw
+// values (q, k weighted; v plain), RoPE on q and k, and the q_out / ring-cache stores
+// (generate_references.py:265-274; sliding/rmsnorm.rs:22-153, rope.rs:9-211, ops.rs:72-75).
+// Thread t owns head element t; RoPE partners (t, t ^ 128) meet in LDS. A bad offset writes
+// nothing; workgroup (0, 0) reports it.
+template <ScaleKind SK>
+__global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, int m0, int M,
+                                                                   const float* __restrict__ part, int splits,
                                                                    uint32_t* err) {
     __shared__ float red[4];
     __shared__ float xch[kDs];
@@ -256,11 +361,16 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
     }
     const int slot = (kv_off / (kNs * kDs * 2) + mm) % kTs;
     const int trow = rope_off / (kDs * 2) + mm;
+    const int col = head * kDs + t;
+    float acc = 0.0f;
+    for (int z = 0; z < splits; ++z) acc += part[((size_t)z * M + m) * kQkvRowsTotal + col];
+    const float sc = head < 16 ? chunk_scale<SK>(p.qs, col)
+                               : (head < 24 ? chunk_scale<SK>(p.ks, col - kQs) : chunk_scale<SK>(p.vs, col - kQs - kPs));
+    const float v = rbf(acc * sc);
     const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
     const float wv = wn ? bf2f(wn[t]) : 1.0f;
     const float cv = bf2f(p.cos[(size_t)trow * kDs + t]);
     const float sv = bf2f(p.sin[(size_t)trow * kDs + t]);
-    const float v = bf2f(raw[(size_t)m * kQkvRowsTotal + head * kDs + t]);
     const float inv = rms_inverse(ck_block_sum(v * v, red), kDs);
     float n = v * inv;
     if (wn) n = n * wv;
@@ -296,12 +406,19 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
     for (int i = 0; i < 2; ++i) {
         const int c = min(t + 256 * i, NC - 1);
         const bool act = t + 256 * i < NC;
+        float a[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.0f;
+        for (int z = 0; z < splits; ++z) {
+            const float* src = part + ((size_t)z * M + m) * kH + c * 8;
+            const float4 u = *reinterpret_cast<const float4*>(src);
+            const float4 v = *reinterpret_cast<const float4*>(src + 4);
+            a[0] += u.x; a[1] += u.y; a[2] += u.z; a[3] += u.w;
+            a[4] += v.x; a[5] += v.y; a[6] += v.z; a[7] += v.w;
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int n = c * 8 + e;
-            float a = 0.0f;
-            for (int z = 0; z < splits; ++z) a += part[((size_t)z * M + m) * kH + n];
-            d[i][e] = rbf(a * chunk_scale<SK>(scale, n));
+            d[i][e] = rbf(a[e] * chunk_scale<SK>(scale, c * 8 + e));
             if (act) ss = fmaf(d[i][e], d[i][e], ss);
         }
     }
@@ -335,11 +452,35 @@ hipError_t ck_launch(K kernel, dim3 grid, hipStream_t s, A... args) {
     return hipGetLastError();
 }
 
-template <Epi E>
-hipError_t gemm(const GemmArgs& g, int splits, ScaleKind sk, hipStream_t s) {
+// Split-K factor: the largest of 1, 2, 4, 8 that divides the 64-k steps, keeps the grid near one
+// workgroup per CU and fits the partial-sum buffer.
+int pick_splits(int tiles, int ksteps, size_t rows_x_cols) {
+    int sp = 1;
+    for (int c = 2; c <= 8; c *= 2)
+        if (ksteps % c == 0 && tiles * c <= kCkTilesTarget && (size_t)c * rows_x_cols <= kChunkPartFloats) sp = c;
+    return sp;
+}
+
+hipError_t gemm_partial(const GemmArgs& g, int splits, ScaleKind sk, hipStream_t s) {
+    if (g.N % kCkBN || g.K % (kCkBK * splits) || (size_t)splits * g.M * g.N > kChunkPartFloats) return hipErrorInvalidValue;
     const dim3 grid(g.N / kCkBN, (g.M + kCkBM - 1) / kCkBM, splits);
-    return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<E, ScaleKind::F32>, grid, s, g)
-                                : ck_launch(chunk_gemm_kernel<E, ScaleKind::BF16>, grid, s, g);
+    return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32>, grid, s, g)
+                                : ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::BF16>, grid, s, g);
+}
+
+hipError_t gemm_geglu(const GemmArgs& g, ScaleKind sk, hipStream_t s) {
+    if (g.N % 64 || g.K % kCkBK) return hipErrorInvalidValue;
+    const dim3 grid(g.N / 64, (g.M + kCkBM - 1) / kCkBM, 1);
+    return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<Epi::GeGLU, ScaleKind::F32>, grid, s, g)
+                                : ck_launch(chunk_gemm_kernel<Epi::GeGLU, ScaleKind::BF16>, grid, s, g);
+}
+
+int m_tiles(int M) { return (M + kCkBM - 1) / kCkBM; }
+
+template <ScaleKind SK>
+hipError_t post_rows(const float* part, int splits, int M, const void* scale, const uint16_t* w_post, uint16_t* res,
+                     const uint16_t* ls, hipStream_t s) {
+    return ck_launch(chunk_post_rows_kernel<SK>, dim3(M), s, part, splits, M, scale, w_post, res, ls);
 }
 
 }  // namespace
@@ -348,29 +489,32 @@ hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, De
     hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel, dim3(M), s, p.x + (size_t)m0 * kH, p.in_rms, ctx->hbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
-    g.x = ctx->hbuf; g.ldx = kH; g.M = M; g.N = kQkvRowsTotal; g.K = kH;
+    g.x = ctx->hbuf; g.M = M; g.N = kQkvRowsTotal; g.K = kH;
     g.w[0] = p.qw; g.w[1] = p.kw; g.w[2] = p.vw;
-    g.s[0] = p.qs; g.s[1] = p.ks; g.s[2] = p.vs;
     g.nseg[0] = 0; g.nseg[1] = kQs; g.nseg[2] = kQs + kPs; g.nseg[3] = kQkvRowsTotal; g.nsegs = 3;
-    g.y = ctx->raw_qkv; g.ldy = kQkvRowsTotal;
-    e = gemm<Epi::Bf16Scaled>(g, 1, p.scale_kind, s);
+    g.yf = ctx->fbuf;
+    const int sp = pick_splits(kQkvRowsTotal / kCkBN * m_tiles(M), kH / kCkBK, (size_t)M * kQkvRowsTotal);
+    e = gemm_partial(g, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
-    return ck_launch(chunk_qkv_heads_kernel, dim3(32, M), s, p, m0, (const uint16_t*)ctx->raw_qkv, ctx->err);
+    return p.scale_kind == ScaleKind::F32
+        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32>, dim3(32, M), s, p, m0, M, (const float*)ctx->fbuf, sp, ctx->err)
+        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16>, dim3(32, M), s, p, m0, M, (const float*)ctx->fbuf, sp, ctx->err);
 }
 
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    hipError_t e = ck_launch(chunk_tile_rows_kernel, dim3(M), s, p.x + (size_t)m0 * kQs, kQs, ctx->pbuf);
+    if (e != hipSuccess) return e;
     GemmArgs g{};
-    g.x = p.x + (size_t)m0 * kQs; g.ldx = kQs; g.M = M; g.N = kH; g.K = kQs;
-    g.w[0] = p.ow; g.s[0] = p.os; g.nseg[0] = 0; g.nseg[1] = kH; g.nsegs = 1;
+    g.x = ctx->pbuf; g.M = M; g.N = kH; g.K = kQs;
+    g.w[0] = p.ow; g.nseg[0] = 0; g.nseg[1] = kH; g.nsegs = 1;
     g.yf = ctx->fbuf;
-    hipError_t e = gemm<Epi::F32Partial>(g, kChunkSplitK, p.scale_kind, s);
+    const int sp = pick_splits(kH / kCkBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
+    e = gemm_partial(g, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
     uint16_t* res = p.residual + (size_t)m0 * kH;
     return p.scale_kind == ScaleKind::F32
-        ? ck_launch(chunk_post_rows_kernel<ScaleKind::F32>, dim3(M), s, (const float*)ctx->fbuf, kChunkSplitK, M, p.os,
-                    p.post_rms, res, (const uint16_t*)nullptr)
-        : ck_launch(chunk_post_rows_kernel<ScaleKind::BF16>, dim3(M), s, (const float*)ctx->fbuf, kChunkSplitK, M, p.os,
-                    p.post_rms, res, (const uint16_t*)nullptr);
+        ? post_rows<ScaleKind::F32>(ctx->fbuf, sp, M, p.os, p.post_rms, res, nullptr, s)
+        : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.os, p.post_rms, res, nullptr, s);
 }
 
 hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
@@ -379,23 +523,21 @@ hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, De
     hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel, dim3(M), s, (const uint16_t*)res, p.pre_rms, ctx->hbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
-    g.x = ctx->hbuf; g.ldx = kH; g.M = M; g.N = kL; g.K = kH;
-    g.w[0] = p.up; g.s[0] = p.up_s; g.nseg[0] = 0; g.nseg[1] = kL; g.nsegs = 1;
-    g.w2 = p.gate; g.s2 = p.gate_s;
-    g.y = ctx->pbuf; g.ldy = kL;
-    e = gemm<Epi::GeGLU>(g, 1, p.scale_kind, s);
+    g.x = ctx->hbuf; g.M = M; g.N = kL; g.K = kH;
+    g.w[0] = p.up; g.w2 = p.gate; g.s0 = p.up_s; g.s2 = p.gate_s;
+    g.y = ctx->pbuf;
+    e = gemm_geglu(g, p.scale_kind, s);
     if (e != hipSuccess) return e;
     GemmArgs d{};
-    d.x = ctx->pbuf; d.ldx = kL; d.M = M; d.N = kH; d.K = kL;
-    d.w[0] = p.down; d.s[0] = p.down_s; d.nseg[0] = 0; d.nseg[1] = kH; d.nsegs = 1;
+    d.x = ctx->pbuf; d.M = M; d.N = kH; d.K = kL;
+    d.w[0] = p.down; d.nseg[0] = 0; d.nseg[1] = kH; d.nsegs = 1;
     d.yf = ctx->fbuf;
-    e = gemm<Epi::F32Partial>(d, kChunkSplitK, p.scale_kind, s);
+    const int sp = pick_splits(kH / kCkBN * m_tiles(M), kL / kCkBK, (size_t)M * kH);
+    e = gemm_partial(d, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
     return p.scale_kind == ScaleKind::F32
-        ? ck_launch(chunk_post_rows_kernel<ScaleKind::F32>, dim3(M), s, (const float*)ctx->fbuf, kChunkSplitK, M, p.down_s,
-                    p.post_rms, res, p.layer_scalar)
-        : ck_launch(chunk_post_rows_kernel<ScaleKind::BF16>, dim3(M), s, (const float*)ctx->fbuf, kChunkSplitK, M, p.down_s,
-                    p.post_rms, res, p.layer_scalar);
+        ? post_rows<ScaleKind::F32>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s)
+        : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
 }
 
 }  // namespace moa

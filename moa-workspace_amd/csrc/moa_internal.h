@@ -13,9 +13,10 @@ constexpr int kMaxDecodeM = 16;
 // Rows handled by one call of the MFMA (M > kMaxDecodeM) path; larger calls are tiled by the host.
 constexpr int kMaxChunkM = 1024;
 // K splits of the MFMA path's 3840-wide projections (O, FFN down).
-constexpr int kChunkSplitK = 2;
 // QKV projection rows (Q | K | V).
 constexpr int kQkvRowsTotal = kQs + 2 * kPs;
+// f32 split-K partial sums of the MFMA path: splits x M x N never exceeds one chunk of QKV columns
+constexpr size_t kChunkPartFloats = (size_t)kMaxChunkM * kQkvRowsTotal;
 
 // Arrival counters. Each counter owns a 256-byte line: device-scope atomics to one line
 // serialise (~15 ns each), so counters never share a line and each kernel arrives once per
@@ -56,7 +57,7 @@ struct DevCtx {
     uint16_t* pbuf = nullptr;     // [kMaxChunkM, 15360] bf16 (O: [M,3840]; FFN: GeGLU output)
     uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
-    float* fbuf = nullptr;        // [kChunkSplitK, kMaxChunkM, 3840] f32 split-K partial sums (MFMA path)
+    float* fbuf = nullptr;        // [splits][M][N] f32 split-K partial sums (MFMA path), kChunkPartFloats
     uint64_t* ffn_part = nullptr; // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)

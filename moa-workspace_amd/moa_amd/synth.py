@@ -212,6 +212,18 @@ def cfg_qkv(seed: int = 0, M: int = 1, tag: str = "cfg2", theta: float = 10_000.
                 k_cache=bf16_normal(n("k_cache"), (TS, NS, DS)), v_cache=bf16_normal(n("v_cache"), (TS, NS, DS)))
 
 
+def cfg_layer_chunk(seed: int = 0, M: int = 256, tag: str = "cfg4") -> dict:
+    """Config 4's activations: one decoder-layer chunk of M prefill rows at positions 0..M-1
+    (ring slots 0..M-1, other slots pre-filled N(0,1)); the attention output that feeds the
+    O-projection is a seeded N(0,1) bf16 input. The FP8 weights are those of configs 0-2 (same
+    shapes and distributions)."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    cos, sin = rope_tables(range(0, M), 10_000.0)
+    return dict(x=bf16_normal(n("x"), (M, H)), attn=bf16_normal(n("attn"), (M, QS)), pos=0, rope_offset=0,
+                kv_offset=0, cos=cos, sin=sin,
+                k_cache=bf16_normal(n("k_cache"), (TS, NS, DS)), v_cache=bf16_normal(n("v_cache"), (TS, NS, DS)))
+
+
 def cfg_ffn_mxfp4(seed: int = 0, M: int = 1, tag: str = "cfg3") -> dict:
     """Config 3: MXFP4 FFN (E2M1 + E8M0 per 32 along K)."""
     n = lambda t: f"{tag}.seed{seed}.{t}"
