@@ -26,8 +26,9 @@ constexpr int kCkBlock = 256;          // four waves
 constexpr int kCkBM = 256;             // rows per workgroup: wave w takes rows 64 w .. 64 w + 63
 constexpr int kCkBN = 128;             // weight rows per workgroup (GeGLU: 64 up + the same 64 gate)
 constexpr int kCkBK = 64;              // k per pipeline step
-constexpr int kCkWStride = kCkBK + 16; // LDS bytes per staged weight row: 80 puts 16 rows on distinct banks
+constexpr int kCkWStride = 2 * kCkBK + 16;  // LDS bytes per staged (bf16) weight row: 144 puts 16 rows on distinct banks
 constexpr int kCkTilesTarget = 264;    // split-K aims at about one workgroup per CU
+constexpr int kCkSplitMax = 8;
 
 // 8 E4M3 codes (two dwords, lower index in the low byte) widened to 8 bf16.
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
@@ -96,10 +97,10 @@ constexpr int kCkNt = 2;  // cache policy: non-temporal (weights are read once)
 //   of the step takes k 32 h + 8 j .. + 7 from lane half h, for A and B alike, which is a fixed
 //   permutation of the step's 64 k. Row blocks past M read zeros (the buffer ends there); rows
 //   past M are not stored.
-//   Weights (FP8) are staged once per workgroup through LDS: each thread moves two 16-byte chunks
-//   per step, loaded eight steps ahead (HBM latency at the rate the whole chip streams weights)
-//   and written two steps ahead; a wave reads
-//   32 bytes per lane per 32-column block and widens them to bf16 (exact for E4M3).
+//   Weights (FP8) are staged once per workgroup through LDS, widened to bf16 on the way (exact for
+//   E4M3; once per workgroup instead of once per wave): each thread moves two 16-byte chunks per
+//   step, loaded eight steps ahead (HBM latency at the rate the whole chip streams weights) and
+//   written two steps ahead; a wave reads 64 bytes (bf16) per lane per 32-column block.
 //   All loads are buffer loads whose per-lane offsets are fixed: the step moves the scalar
 //   offset only. Prefetches past the last step repeat the last step (harmless), so the loop body
 //   has no branches.
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         wvo[0] = r0 * g.K + kbeg + 16 * q;
         wvo[1] = (r0 + 64) * g.K + kbeg + 16 * q;
     }
-    const int wdst0 = r0 * kCkWStride + 16 * q, wdst1 = (r0 + 64) * kCkWStride + 16 * q;
+    const int wdst0 = r0 * kCkWStride + 32 * q, wdst1 = (r0 + 64) * kCkWStride + 32 * q;
 
     const int kst = g.K / kCkBK;  // 64-k steps (A tiles) per row block
     const int rblks = (min(g.M - m_blk, kCkBM) + 31) >> 5;
@@ -152,9 +153,8 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
 
     constexpr int WD = 6;  // weight register sets: W(s + 2) is loaded six steps before it is staged
     uint4 wr[WD][2];       // [set][row pair]
-    uint4 ar[2][2][4];     // [set][32-row block][16 bytes]
-    uint4 braw[2][2];      // FP8 B fragments as read from LDS: [set][32 bytes]
-    bf16x8 bb[2][4];       // widened: [set][MFMA j]
+    uint4 ar[3][2][4];     // [set][32-row block][16 bytes]: A(s) in set s mod 3, loaded two steps ahead
+    bf16x8 bb[2][4];       // B fragments: [set][MFMA j]
     const int last = nsteps - 1;
     auto load_w = [&](uint4 (&dst)[2], int s) {
         const int so = min(s, last) * kCkBK;
@@ -162,8 +162,12 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[1], wvo[1], so, kCkNt));
     };
     auto store_w = [&](const uint4 (&src)[2], int buf) {
-        *reinterpret_cast<uint4*>(&ws[buf][wdst0]) = src[0];
-        *reinterpret_cast<uint4*>(&ws[buf][wdst1]) = src[1];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            bf16x8* d = reinterpret_cast<bf16x8*>(&ws[buf][i ? wdst1 : wdst0]);
+            d[0] = fp8x8_to_bf16(src[i].x, src[i].y);
+            d[1] = fp8x8_to_bf16(src[i].z, src[i].w);
+        }
     };
     auto load_a = [&](uint4 (&dst)[2][4], int s) {
         const int so = min(s, last) * 4096;
@@ -173,16 +177,10 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
             for (int i = 0; i < 4; ++i)
                 dst[mb][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ars, avo[mb] + 1024 * i, so, 0));
     };
-    auto read_b = [&](uint4 (&dst)[2], int buf, int nb) {
-        const uint8_t* bp = &ws[buf][(32 * nb + l32) * kCkWStride + 32 * hf];
-        dst[0] = *reinterpret_cast<const uint4*>(bp);
-        dst[1] = *reinterpret_cast<const uint4*>(bp + 16);
-    };
-    auto widen = [&](bf16x8 (&dst)[4], const uint4 (&src)[2]) {
-        dst[0] = fp8x8_to_bf16(src[0].x, src[0].y);
-        dst[1] = fp8x8_to_bf16(src[0].z, src[0].w);
-        dst[2] = fp8x8_to_bf16(src[1].x, src[1].y);
-        dst[3] = fp8x8_to_bf16(src[1].z, src[1].w);
+    auto read_b = [&](bf16x8 (&dst)[4], int buf, int nb) {
+        const bf16x8* bp = reinterpret_cast<const bf16x8*>(&ws[buf][(32 * nb + l32) * kCkWStride + 64 * hf]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[j] = bp[j];
     };
     auto mfma8 = [&](const uint4 (&a)[2][4], const bf16x8 (&b)[4], auto NB) {
         constexpr int nb = decltype(NB)::value;
@@ -196,37 +194,83 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     // Three LDS buffers: step s reads buffer s mod 3 and stages W(s + 2) into buffer (s + 2) mod 3
     // (last read in step s - 1, before the barrier that opens step s), so the first fragment of
     // step s + 1 (buffer (s + 1) mod 3, staged in step s - 1) is read before step s ends. Within a
-    // step, fragment nb + 1 is widened while fragment nb's eight MFMAs run.
+    // step, fragment nb + 1 is read while fragment nb's eight MFMAs run.
 #pragma unroll
     for (int i = 0; i < WD; ++i) load_w(wr[i], i);
     load_a(ar[0], 0);
+    load_a(ar[1], 1);
     store_w(wr[0], 0);
     store_w(wr[1], 1);
     load_w(wr[0], WD);
     load_w(wr[1], WD + 1);
     __syncthreads();
-    read_b(braw[0], 0, 0);
+    read_b(bb[0], 0, 0);
     auto body = [&](auto P, int s) {
         constexpr int c = decltype(P)::value;  // s mod 6
         constexpr int cb = c % 3, nbuf = (c + 1) % 3;
-        const uint4(&a)[2][4] = ar[c & 1];
-        load_a(ar[(c + 1) & 1], s + 1);
+        const uint4(&a)[2][4] = ar[c % 3];
+        // Fences fix the issue order: each fragment's LDS reads go out during the previous
+        // fragment's eight MFMAs, one or two other instructions after each MFMA (a single wave
+        // per SIMD issues them while the MFMA runs); the A prefetch rides with fragment 0, the
+        // weight staging (16 widenings, 4 LDS writes, 2 loads) with fragment 1.
+        constexpr int kDsR = 0x100, kDsW = 0x200, kVmR = 0x020, kValu = 0x002, kMfma = 0x008;
+        read_b(bb[1], cb, 1);
+        load_a(ar[(c + 2) % 3], s + 2);
+        mfma8(a, bb[0], Par<0>{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kDsR, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kVmR, 2, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(bb[0], cb, 2);
         store_w(wr[(c + 2) % WD], (c + 2) % 3);
         load_w(wr[(c + 2) % WD], s + 2 + WD);
-        __builtin_amdgcn_sched_barrier(0);
-        widen(bb[0], braw[0]);
-        read_b(braw[1], cb, 1);
-        mfma8(a, bb[0], Par<0>{});
-        widen(bb[1], braw[1]);
-        read_b(braw[0], cb, 2);
         mfma8(a, bb[1], Par<1>{});
-        widen(bb[0], braw[0]);
-        read_b(braw[1], cb, 3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kDsR, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kValu, 2, 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kValu, 2, 1);
+            __builtin_amdgcn_sched_group_barrier(kDsW, 1, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(kVmR, 2, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(bb[1], cb, 3);
         mfma8(a, bb[0], Par<2>{});
-        widen(bb[1], braw[1]);
-        read_b(braw[0], nbuf, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 2);
+            __builtin_amdgcn_sched_group_barrier(kDsR, 1, 2);
+        }
+        __builtin_amdgcn_sched_group_barrier(kMfma, 4, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        read_b(bb[0], nbuf, 0);
         mfma8(a, bb[1], Par<3>{});
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 3);
+            __builtin_amdgcn_sched_group_barrier(kDsR, 1, 3);
+        }
+        __builtin_amdgcn_sched_group_barrier(kMfma, 4, 3);
+        // Step barrier. Every read of the buffer the next step overwrites fed an MFMA of this step
+        // (so it is complete); the next step's buffer needs this wave's LDS writes complete, and
+        // only the four reads just issued may still be in flight: lgkmcnt(4), not 0.
+        __builtin_amdgcn_sched_barrier(0);
+        __asm__ volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     };
     int s = 0;
     for (; s + 5 < nsteps; s += 6) {
@@ -362,8 +406,12 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
     const int slot = (kv_off / (kNs * kDs * 2) + mm) % kTs;
     const int trow = rope_off / (kDs * 2) + mm;
     const int col = head * kDs + t;
-    float acc = 0.0f;
-    for (int z = 0; z < splits; ++z) acc += part[((size_t)z * M + m) * kQkvRowsTotal + col];
+    float pz[kCkSplitMax];  // all partial loads in flight at once (index clamped), summed in split order
+#pragma unroll
+    for (int z = 0; z < kCkSplitMax; ++z) pz[z] = part[((size_t)min(z, splits - 1) * M + m) * kQkvRowsTotal + col];
+    float acc = pz[0];
+#pragma unroll
+    for (int z = 1; z < kCkSplitMax; ++z) acc = z < splits ? acc + pz[z] : acc;
     const float sc = head < 16 ? chunk_scale<SK>(p.qs, col)
                                : (head < 24 ? chunk_scale<SK>(p.ks, col - kQs) : chunk_scale<SK>(p.vs, col - kQs - kPs));
     const float v = rbf(acc * sc);
@@ -406,15 +454,22 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
     for (int i = 0; i < 2; ++i) {
         const int c = min(t + 256 * i, NC - 1);
         const bool act = t + 256 * i < NC;
-        float a[8];
+        // all partial loads in flight at once (index clamped), then summed in split order
+        float4 u[kCkSplitMax], v[kCkSplitMax];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = 0.0f;
-        for (int z = 0; z < splits; ++z) {
-            const float* src = part + ((size_t)z * M + m) * kH + c * 8;
-            const float4 u = *reinterpret_cast<const float4*>(src);
-            const float4 v = *reinterpret_cast<const float4*>(src + 4);
-            a[0] += u.x; a[1] += u.y; a[2] += u.z; a[3] += u.w;
-            a[4] += v.x; a[5] += v.y; a[6] += v.z; a[7] += v.w;
+        for (int z = 0; z < kCkSplitMax; ++z) {
+            const float* src = part + ((size_t)min(z, splits - 1) * M + m) * kH + c * 8;
+            u[z] = *reinterpret_cast<const float4*>(src);
+            v[z] = *reinterpret_cast<const float4*>(src + 4);
+        }
+        float a[8] = {u[0].x, u[0].y, u[0].z, u[0].w, v[0].x, v[0].y, v[0].z, v[0].w};
+#pragma unroll
+        for (int z = 1; z < kCkSplitMax; ++z) {
+            const bool on = z < splits;
+            a[0] = on ? a[0] + u[z].x : a[0]; a[1] = on ? a[1] + u[z].y : a[1];
+            a[2] = on ? a[2] + u[z].z : a[2]; a[3] = on ? a[3] + u[z].w : a[3];
+            a[4] = on ? a[4] + v[z].x : a[4]; a[5] = on ? a[5] + v[z].y : a[5];
+            a[6] = on ? a[6] + v[z].z : a[6]; a[7] = on ? a[7] + v[z].w : a[7];
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -456,7 +511,7 @@ hipError_t ck_launch(K kernel, dim3 grid, hipStream_t s, A... args) {
 // workgroup per CU and fits the partial-sum buffer.
 int pick_splits(int tiles, int ksteps, size_t rows_x_cols) {
     int sp = 1;
-    for (int c = 2; c <= 8; c *= 2)
+    for (int c = 2; c <= kCkSplitMax; c *= 2)
         if (ksteps % c == 0 && tiles * c <= kCkTilesTarget && (size_t)c * rows_x_cols <= kChunkPartFloats) sp = c;
     return sp;
 }
