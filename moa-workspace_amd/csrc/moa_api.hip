@@ -54,6 +54,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_opart = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
+    const size_t t_ptag = carve(sizeof(uint64_t) * (kL / 2));
     int cus = 0;
     *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (*err != hipSuccess) return nullptr;
@@ -79,6 +80,7 @@ DevCtx* device_context(hipError_t* err) {
     c.ffn_part = reinterpret_cast<uint64_t*>(b + t_part);
     c.o_part = reinterpret_cast<uint64_t*>(b + t_opart);
     c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
+    c.ffn_ptag = reinterpret_cast<uint64_t*>(b + t_ptag);
     c.base = base;
     return &c;
 }

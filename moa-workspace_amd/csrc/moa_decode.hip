@@ -1179,20 +1179,29 @@ __global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, c
 // Two grid-wide dependencies: every down row needs all 15360 GeGLU values (p), and the post-norm
 // of every output needs the sum of squares of all 3840 down outputs.
 //
-// p: wave 7 (the control wave) publishes the workgroup's GeGLU values and arrives on a barrier --
-// a 16-leaf arrival tree plus a generation word that moves by one per launch: the control wave
-// reads it at entry (g0); the workgroup that completes the tree resets the tree and stores
-// g0 + 1; the others poll until it reads g0 + 1 -- then stages p into LDS. Waves 0-6 issue the
-// first kFfnDownPre chunks of their down rows before the barrier, so the down weight stream
-// follows the up/gate stream. The control wave issues its own down loads only after staging p:
-// a CU serves its loads in order, so a wave with weight loads in flight would see the barrier
-// only once they had landed.
+// p, FP8 weights: tagged words instead of a barrier. Every workgroup's control wave publishes the
+// workgroup's 64 GeGLU values as 32 64-bit words (two bf16 values and the launch's tag). It issues
+// them before any other load of the workgroup: a CU serves its loads in order, so the words are
+// not queued behind the workgroup's weight loads. Then every thread issues its first read of p
+// (15 words; workgroups start at different words so that they do not all request one line), and
+// every wave issues its first kFfnDownPre down chunks. Words that do not yet carry the tag are read
+// again until they do. No atomic arrival or poll sits between the last workgroup's up/gate rows and
+// everyone's p.
+// p, FP4 weights: a barrier. The control wave publishes, then arrives on a 16-leaf arrival tree
+// plus a generation word that moves by one per launch: the control wave reads it at entry (g0);
+// the workgroup that completes the tree resets the tree and stores g0 + 1; the others poll until
+// it reads g0 + 1, then stage p into LDS. Waves 0-6 issue their first kFfnDownPre down chunks
+// before the barrier. The control wave issues its own only after staging p, since a wave with
+// weight loads in flight would see the barrier only once they had landed.
+// The launch's tag is ep + 1: 16 counters, each advanced by 15 workgroups per launch of any format,
+// give ep. Tags therefore never repeat across launches, so a word left by an earlier launch never
+// carries the current tag.
 //
 // Post-norm: every workgroup publishes its 16 down outputs and its partial sum of squares, each
-// 64-bit word tagged with g0 + 1 (a word holding the tag is complete, so no counters), and is
-// done. The kPostLeaders leader workgroups poll the tags: leader g sums all 240 partials in a fixed
-// order (deterministic, the same bits in every leader) and writes the outputs of the workgroups
-// b = g (mod kPostLeaders). Few pollers keep the tagged lines free of contention.
+// 64-bit word carrying the launch's tag (a word holding the tag is complete, so no counters), and
+// is done. The kPostLeaders leader workgroups poll the tags. Leader g sums all 240 partials in a
+// fixed order (deterministic, the same bits in every leader) and writes the outputs of the
+// workgroups b = g (mod kPostLeaders). Few pollers keep the tagged lines free of contention.
 //
 // Every poll is bounded by the wall clock (kSpinTicks): on expiry it sets kErrSpinTimeout in the
 // device error word and carries on, so every wave exits even if the grid were not resident.
@@ -1202,7 +1211,8 @@ constexpr int kFfnGrid = kL / (kFfnWaves * kUgRL);  // 240 workgroups
 constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgroup
 constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
 constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
-constexpr int kFfnDownPre = 6;                      // down chunks per row loaded before the first barrier
+constexpr int kFfnDownPre = 4;                      // down chunks per row loaded before p is staged
+constexpr int kFfnEpochCounters = 16;               // launch-epoch counters (15 workgroups each)
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
 static_assert(kFfnGrid == kPostGrid && kFfnWgRows == kPostWgRows, "post-norm hand-off shape");
 
@@ -1234,19 +1244,27 @@ __device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint
 
 template <FfnFormat F, ScaleKind SK>
 __global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, PostSlots* slots, uint32_t* tickets, uint32_t* err) {
+void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostSlots* slots, uint32_t* tickets,
+                      uint32_t* err) {
     constexpr int KD = down_chunks<F>();
     constexpr int EPC = elems_per_chunk<F>();
     __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
     __shared__ float red[kFfnWaves];
     __shared__ float pl[kFfnWaves * kUgRL];
     __shared__ uint32_t dl[kFfnWgRows];  // the workgroup's down outputs (bf16 bits)
+    __shared__ uint32_t s_tag;
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
     const bool leader = blockIdx.x < kPostLeaders;
     uint32_t* gen = tickets + kTicketFfnGen * kTicketStride;
     uint32_t g0 = 0;
     if (ctl) g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The launch's tag: 16 counters of 15 workgroups each advance by one per launch (every format
+    // shares them, so post-norm slot tags never repeat across formats). Needed only after up/gate.
+    uint32_t ep = 0;
+    if (ctl && lane == 0)
+        ep = counter_add(tickets + (kTicketFfnEpoch + blockIdx.x % kFfnEpochCounters) * kTicketStride) /
+             (kFfnGrid / kFfnEpochCounters);
     uint16_t* res = p.residual + (size_t)m0 * kH;
     const bool post = p.post_rms != nullptr;
 
@@ -1272,14 +1290,53 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, PostSlots* slots, uin
     const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
     const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red);
     if (lane < kUgRL) pl[lane * kFfnWaves + wave] = pv;
+    if (ctl && lane == 0) s_tag = ep + 1u;
     __syncthreads();  // pl complete; every wave has read its x out of sh
+    const uint32_t tag = s_tag;
 
     // Down loads only once the whole workgroup is through its up/gate rows (issued earlier they
     // would queue ahead of the slower waves' up/gate loads, which the barrier waits for).
     constexpr int PD = kFfnDownPre < KD ? kFfnDownPre : KD;
     constexpr int RS = PD < KD ? PD + 1 : KD;  // ring slots
     Chunk<F> ring[RS][kFfnDownR];
-    if (!ctl) {
+    if constexpr (F == FfnFormat::FP8) {
+        // p by tagged words instead of a barrier. The control wave's 32 words (two GeGLU values and
+        // the launch's tag each) are issued before any other load of the workgroup: a CU serves
+        // its loads in order, so they are not queued behind this workgroup's weight loads. Every
+        // thread then issues its first read of p, then every wave (the control wave too) its
+        // first PD down chunks; words not yet current are read again until they are.
+        if (ctl && lane < kFfnWaves * kUgRL / 2)
+            publish64(ptag + blockIdx.x * (kFfnWaves * kUgRL / 2) + lane,
+                      tagged(tag, f2bf(pl[2 * lane]) | (f2bf(pl[2 * lane + 1]) << 16)));
+        __syncthreads();  // the publish is issued ahead of every load below
+        constexpr int PW = kL / 2 / kFfnBlock;  // 15 words per thread
+        static_assert(PW * kFfnBlock == kL / 2, "p words per thread");
+        // word w of thread t in read i: workgroups start at different words (rotation by 32 b), so
+        // that 240 readers of the same 61 KB do not request the same lines at the same time
+        auto pword = [&](int i) { return (threadIdx.x + kFfnBlock * i + blockIdx.x * 32) % (kL / 2); };
+        uint64_t pw[PW];
+#pragma unroll
+        for (int i = 0; i < PW; ++i) pw[i] = collect64(ptag + pword(i));
+#pragma unroll
+        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
+        const uint64_t t0 = wall_clock64();
+        for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < PW; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
+            if (__all(ok)) break;
+            if (wall_clock64() - t0 > kSpinTicks) {
+                if (lane == 0) atomicOr(err, kErrSpinTimeout);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < PW; ++i)
+                if ((uint32_t)(pw[i] >> 32) != tag) pw[i] = collect64(ptag + pword(i));
+        }
+#pragma unroll
+        for (int i = 0; i < PW; ++i) *reinterpret_cast<uint32_t*>(sh + 2 * pword(i)) = (uint32_t)pw[i];
+    } else if (!ctl) {
 #pragma unroll
         for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
     } else {
@@ -1300,7 +1357,7 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, PostSlots* slots, uin
     __syncthreads();  // p staged
 
     // ---- down: the ring streams the rest of the rows while the dots run
-    if (ctl) {  // issued after the barrier so that no other wave waits on these issues
+    if (F != FfnFormat::FP8 && ctl) {  // issued after the barrier so that no other wave waits on these issues
 #pragma unroll
         for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
     }
@@ -1343,7 +1400,6 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, PostSlots* slots, uin
         }
         return;
     }
-    const uint32_t tag = g0 + 1u;
     post_publish(slots, tag, dl, lane);
     if (!leader) return;
     post_leader(slots, tag, res, r8, w8, p.layer_scalar != nullptr, lsv, lane, err);
@@ -1499,7 +1555,7 @@ static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevC
         hipError_t e;
         if (mm == 1 && ffn_fused_fits<F, SK>(ctx)) {
             ffn_fused_kernel<F, SK><<<dim3(kFfnGrid), dim3(kFfnBlock), 0, s>>>(
-                p, m0, ctx->pbuf, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
+                p, m0, ctx->pbuf, ctx->ffn_ptag, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
             continue;

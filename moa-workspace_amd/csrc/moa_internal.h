@@ -35,7 +35,8 @@ constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
 // reset; a workgroup adds one at entry and divides what it read by the workgroups per counter.
 constexpr int kTicketOEpoch = kTicketFfnGen + 1;
 constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
-constexpr int kTicketCount = kTicketQkvEpoch + 32;
+constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN workgroups each
+constexpr int kTicketCount = kTicketFfnEpoch + 16;
 
 // Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
 // never shared with another kernel).
@@ -58,7 +59,8 @@ struct DevCtx {
     uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
     float* fbuf = nullptr;        // [splits][M][N] f32 split-K partial sums (MFMA path), kChunkPartFloats
-    uint64_t* ffn_part = nullptr; // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
+    uint64_t* ffn_part = nullptr;  // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
+    uint64_t* ffn_ptag = nullptr;  // [kL / 2] tagged GeGLU pairs of the single-launch FP8 FFN (only it writes them)
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
     void* base = nullptr;
