@@ -15,6 +15,9 @@ loop replays its captured layer), preceded by W warm-up steps; HIP events on the
 (the stream the kernels run on) bracket the replays, with synchronisations on both sides.
 Host-driven times (one Python/ctypes call per launch) are reported beside them.
 
+The per-operator list also times sliding_attention (the step between QKV and O, outside the
+headline metric): one token over a full ring (1024 slots), caches rotated like the weights.
+
 Prints one JSON line (stdout). `value` is microseconds per token for the step (lower is better);
 `roofline` is for the dominant operator (the FFN); `cpu_baseline` times the CPU oracle (a C
 restatement of the reference's algorithm) on this host's cores for a bounded sample.
@@ -44,7 +47,9 @@ METRIC = "FFN/QKV/O decode µs/token at M=1 and % of HBM roofline (FP8 weights)"
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec
 MALL_BYTES = 256 << 20
 # Algorithmic bytes per call (weights + scales + operator-boundary vectors).
-BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848}
+BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
+         # sliding_attention, all 1024 slots valid: K and V caches + q + out + mask row
+         "attn": 2 * 1024 * 8 * 256 * 2 + 2 * 4096 * 2 + 1024 * 4}
 GRAPH_CALLS = 40  # calls per captured graph
 # Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
 FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
@@ -63,7 +68,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
-    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "chunk"), default=None,
+    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "chunk"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     args = ap.parse_args()
@@ -83,6 +88,7 @@ def main() -> int:
     ffn = synth.cfg_ffn_fp8(0)
     o = synth.cfg_o(0)
     qkv = synth.cfg_qkv(0)
+    att = synth.cfg_attention(0, M=1, pos=5000)
     log(f"synthesised inputs in {time.time() - t0:.1f}s")
     def dev(a):  # bf16 bits travel as int16 views (torch's uint16 support is partial)
         a = np.ascontiguousarray(a)
@@ -101,6 +107,10 @@ def main() -> int:
     OW = replicate(o, ("o_weight", "o_weight_scale"), no)
     QW = replicate(qkv, ("q_weight", "k_weight", "v_weight", "q_weight_scale", "k_weight_scale",
                          "v_weight_scale"), nq)
+    na = copies(BYTES["attn"])
+    AW = replicate(att, ("k_cache", "v_cache"), na)
+    a_q, a_mask = dev(att["q"]), dev(att["mask"])
+    a_out = torch.zeros(4096, dtype=torch.int16, device="cuda")
     f_res, f_pre, f_post, f_ls = (dev(ffn[k]) for k in ("residual", "pre_ff_rms_weight", "post_ff_rms_weight",
                                                           "layer_scalar"))
     o_x, o_post, o_res = dev(o["x"]), dev(o["post_attn_rms_weight"]), dev(o["residual"])
@@ -161,6 +171,10 @@ def main() -> int:
                                 w["k_weight_scale"], w["v_weight_scale"], q["input_rms_weight"], q["q_rms_weight"],
                                 q["k_rms_weight"], kv, ro, q["cos"], q["sin"], q["k_cache"], q["v_cache"], q_out)
 
+    def run_attn(i):
+        w = AW[i % na]
+        ops.sliding_attention(a_q, w["k_cache"], w["v_cache"], a_mask, a_out)
+
     def run_step(i):
         run_qkv(i)
         run_o(i)
@@ -202,7 +216,7 @@ def main() -> int:
         return a.elapsed_time(b) / (reps * GRAPH_CALLS), reps * GRAPH_CALLS
 
     if args.profile:
-        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "chunk": run_layer}[args.profile]
+        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "chunk": run_layer}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -215,7 +229,7 @@ def main() -> int:
         return 0
 
     per_op = {}
-    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn)):
+    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn)):
         ms, _ = graph_timed(fn, args.steps, args.warmup)
         ms_host = timed(fn, min(args.steps, 50), 5)
         gbps = BYTES[name] / (ms * 1e-3) / 1e9

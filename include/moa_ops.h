@@ -84,6 +84,15 @@ int moa_sliding_project_qkv_bf16_scales(
     const int32_t* kv_offset, const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
     uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M, void* stream);
 
+/* ops::sliding_attention -- FO/src/ops.rs:118-128 (the step between QKV and O).
+ * q bf16 [M,8,2,256] (query heads after head norm and RoPE, the q_out of sliding_project_qkv);
+ * k, v bf16 [1024,8,256] (the ring caches); mask f32 [M,1024] (one row per token row: slot t takes
+ * part when mask[t] != 0, as the runtime's 1.0 / 0.0 rows do, FO/src/host/runtime.rs:160);
+ * out bf16 [M,8,2,256] = softmax over the valid slots of (q . k_t) (scale 1.0) times v
+ * (FO/scripts/reference/gemma4.py:163-186). A row with no valid slot gives zeros. */
+int moa_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                          uint16_t* out, int M, void* stream);
+
 /* ops::sliding_attention_output -- FO/src/ops.rs:130-146.
  * x bf16 [M,4096] (= [M,8,2,256]); post_attn_rms_weight bf16 [3840]; o_weight E4M3
  * [3840,4096]; o_weight_scale f32 [3840]; residual bf16 [M,3840], updated in place:

@@ -55,6 +55,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_opart = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
     const size_t t_ptag = carve(sizeof(uint64_t) * (kL / 2));
+    const size_t t_attn = carve(sizeof(float) * kAttnPartFloats);
     int cus = 0;
     *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (*err != hipSuccess) return nullptr;
@@ -81,6 +82,7 @@ DevCtx* device_context(hipError_t* err) {
     c.o_part = reinterpret_cast<uint64_t*>(b + t_opart);
     c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
     c.ffn_ptag = reinterpret_cast<uint64_t*>(b + t_ptag);
+    c.attn_part = reinterpret_cast<float*>(b + t_attn);
     c.base = base;
     return &c;
 }
@@ -309,6 +311,18 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
                 down_weight_packed, up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
                 nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
     return ffn_common(p, M, stream);
+}
+
+int moa_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask, uint16_t* out,
+                          int M, void* stream) {
+    Check c;
+    c.ptr(q, "q").ptr(k, "k").ptr(v, "v").ptr(mask, "mask", 4).ptr(out, "out").rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return finish(launch_sliding_attention(q, k, v, mask, out, M, static_cast<hipStream_t>(stream), ctx),
+                  "sliding_attention launch");
 }
 
 int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* scale, uint16_t* out,

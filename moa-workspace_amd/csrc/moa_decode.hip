@@ -14,6 +14,8 @@
 //     last-arriving wave, found with a device-scope ticket -- no second launch.
 // blockIdx.y indexes the token row (M <= kMaxDecodeM); rows re-read the same weights, which
 // for small M mostly hit L2/MALL.
+#include <utility>
+
 #include "moa_device.h"
 #include "moa_internal.h"
 
@@ -1216,6 +1218,12 @@ constexpr int kFfnEpochCounters = 16;               // launch-epoch counters (15
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
 static_assert(kFfnGrid == kPostGrid && kFfnWgRows == kPostWgRows, "post-norm hand-off shape");
 
+// Tagged words w[i] whose high half is not `tag` are read again from addr(i).
+template <int N, typename A, int... I>
+__device__ __forceinline__ void reload_stale(uint64_t (&w)[N], uint32_t tag, A addr, std::integer_sequence<int, I...>) {
+    ((w[I] = (uint32_t)(w[I] >> 32) != tag ? collect64(addr(I)) : w[I]), ...);
+}
+
 // One lane per workgroup, after its workgroup's results are published and complete: arrive on
 // `tree` (kTreeCounters counters kTicketStride apart) and wait until `gen` reads `target`.
 __device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint32_t target, uint32_t* err) {
@@ -1330,9 +1338,8 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostS
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int i = 0; i < PW; ++i)
-                if ((uint32_t)(pw[i] >> 32) != tag) pw[i] = collect64(ptag + pword(i));
+            // reload the words still carrying an older tag (unrolled at compile time)
+            reload_stale(pw, tag, [&](int i) { return ptag + pword(i); }, std::make_integer_sequence<int, PW>{});
         }
 #pragma unroll
         for (int i = 0; i < PW; ++i) *reinterpret_cast<uint32_t*>(sh + 2 * pword(i)) = (uint32_t)pw[i];

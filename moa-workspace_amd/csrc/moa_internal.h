@@ -12,7 +12,6 @@ namespace moa {
 constexpr int kMaxDecodeM = 16;
 // Rows handled by one call of the MFMA (M > kMaxDecodeM) path; larger calls are tiled by the host.
 constexpr int kMaxChunkM = 1024;
-// K splits of the MFMA path's 3840-wide projections (O, FFN down).
 // QKV projection rows (Q | K | V).
 constexpr int kQkvRowsTotal = kQs + 2 * kPs;
 // f32 split-K partial sums of the MFMA path: splits x M x N never exceeds one chunk of QKV columns
@@ -36,7 +35,11 @@ constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
 constexpr int kTicketOEpoch = kTicketFfnGen + 1;
 constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
 constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN workgroups each
-constexpr int kTicketCount = kTicketFfnEpoch + 16;
+// sliding_attention: one counter per (row, head) of a launch, 32 arrivals per launch, never reset
+constexpr int kTicketAttn = kTicketFfnEpoch + 16;
+constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;
+// sliding_attention partials: [kMaxDecodeM][kNs][32 chunks][kGs][max, sum, o[kDs]]
+constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (2 + kDs);
 
 // Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
 // never shared with another kernel).
@@ -63,6 +66,7 @@ struct DevCtx {
     uint64_t* ffn_ptag = nullptr;  // [kL / 2] tagged GeGLU pairs of the single-launch FP8 FFN (only it writes them)
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
+    float* attn_part = nullptr;   // sliding_attention split partials (kAttnPartFloats)
     void* base = nullptr;
     int cus = 0;                  // compute units of the device
     int8_t ffn_fused[6] = {-1, -1, -1, -1, -1, -1};  // per (format, scale kind): grid fits resident? (-1 unknown)
@@ -113,6 +117,10 @@ hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s);
 hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);  // FP8 weights
+
+// ops::sliding_attention for M token rows (q / out [M][kNs][kGs][kDs], mask [M][kTs]).
+hipError_t launch_sliding_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const float* mask,
+                                    uint16_t* out, int M, hipStream_t s, DevCtx* ctx);
 
 hipError_t launch_format_selftest(uint32_t* out, hipStream_t s);
 

@@ -83,6 +83,18 @@ def sliding_project_qkv(x, q_weight, k_weight, v_weight, q_weight_scale, k_weigh
     _lib.call(name, *args, M, _stream(x))
 
 
+def sliding_attention(q, k, v, mask, out) -> None:
+    """ops::sliding_attention (FO/src/ops.rs:118-128): out = softmax over the slots with mask != 0 of
+    q . k_t (scale 1.0), times v. q / out [M, 8, 2, 256] bf16, k / v [1024, 8, 256] bf16 (the ring
+    caches), mask [M, 1024] f32."""
+    M = _rows(q, QS, "q")
+    args = [
+        _ptr(q, "q", _BF16), _ptr(k, "k", _BF16, TS * NS * DS), _ptr(v, "v", _BF16, TS * NS * DS),
+        _ptr(mask, "mask", _F32, M * TS), _ptr(out, "out", _BF16, M * QS),
+    ]
+    _lib.call("moa_sliding_attention", *args, M, _stream(q))
+
+
 def sliding_attention_output(x, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
     """ops::sliding_attention_output (FO/src/ops.rs:130-146). Updates residual in place."""
     M = _rows(x, QS, "x")

@@ -224,6 +224,24 @@ def cfg_layer_chunk(seed: int = 0, M: int = 256, tag: str = "cfg4") -> dict:
                 k_cache=bf16_normal(n("k_cache"), (TS, NS, DS)), v_cache=bf16_normal(n("v_cache"), (TS, NS, DS)))
 
 
+def attention_mask(M: int, pos) -> np.ndarray:
+    """The runtime's mask rows (FO/src/host/runtime.rs:160, 409): row min(pos, 1023) has 1.0 at
+    slots <= that row and 0.0 beyond. pos: one position per token row."""
+    pos = np.broadcast_to(np.asarray(pos), (M,))
+    rows = np.minimum(pos, TS - 1)
+    return (np.arange(TS)[None, :] <= rows[:, None]).astype(np.float32)
+
+
+def cfg_attention(seed: int = 0, M: int = 1, pos=1023, q_std: float = 1.0, tag: str = "attn") -> dict:
+    """sliding_attention inputs: q [M, 8, 2, 256] bf16 ~ N(0, q_std) (q after head norm has unit
+    RMS, so q_std = 1 gives the real, peaky scores), ring caches [1024, 8, 256] ~ N(0, 1), and the
+    runtime's mask rows for the given positions."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    return dict(q=bf16_normal(n("q"), (M, NS, QS // (NS * DS), DS), q_std),
+                k_cache=bf16_normal(n("k_cache"), (TS, NS, DS)), v_cache=bf16_normal(n("v_cache"), (TS, NS, DS)),
+                mask=attention_mask(M, pos))
+
+
 def cfg_ffn_mxfp4(seed: int = 0, M: int = 1, tag: str = "cfg3") -> dict:
     """Config 3: MXFP4 FFN (E2M1 + E8M0 per 32 along K)."""
     n = lambda t: f"{tag}.seed{seed}.{t}"

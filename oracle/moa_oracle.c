@@ -345,6 +345,46 @@ void orc_sliding_attention_output(const uint16_t* x, const uint16_t* post_rms, c
     }
 }
 
+/* --------------------------------------------------------------- attention */
+
+/* ops::sliding_attention (FO/src/ops.rs:118-128) against its CPU reference, gemma4.py:163-186:
+ * scaled_dot_product_attention(q, k, v, attn_mask, scale=1.0) for one query position, the mask
+ * being the runtime's 1.0 / 0.0 row over the ring slots (FO/src/host/runtime.rs:160, 409).
+ * Computed in f64 (every bf16 x bf16 product is exact); the output is rounded to f32, then to bf16. A row
+ * with no valid slot gives zeros (the RNGD kernel's sum + 1e-6 gives 0 / 1e-6 = 0 too).
+ * q, out [M][8][2][256]; k, v [1024][8][256]; mask [M][1024]. */
+void orc_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                           uint16_t* out, int M) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int m = 0; m < M; ++m)
+        for (int hq = 0; hq < ORC_NS * ORC_GS; ++hq) {
+            const int n = hq / ORC_GS;
+            const uint16_t* qr = q + ((size_t)m * ORC_NS * ORC_GS + hq) * ORC_DS;
+            const float* mr = mask + (size_t)m * ORC_TS;
+            double s[ORC_TS];
+            double mx = -INFINITY;
+            for (int t = 0; t < ORC_TS; ++t) {
+                if (mr[t] == 0.0f) continue;
+                const uint16_t* kr = k + ((size_t)t * ORC_NS + n) * ORC_DS;
+                double a = 0.0;
+                for (int d = 0; d < ORC_DS; ++d) a += (double)orc_bf16_to_f32(qr[d]) * orc_bf16_to_f32(kr[d]);
+                s[t] = a;
+                if (a > mx) mx = a;
+            }
+            double l = 0.0, o[ORC_DS];
+            for (int d = 0; d < ORC_DS; ++d) o[d] = 0.0;
+            for (int t = 0; t < ORC_TS; ++t) {
+                if (mr[t] == 0.0f) continue;
+                const double p = exp(s[t] - mx);
+                l += p;
+                const uint16_t* vr = v + ((size_t)t * ORC_NS + n) * ORC_DS;
+                for (int d = 0; d < ORC_DS; ++d) o[d] += p * orc_bf16_to_f32(vr[d]);
+            }
+            uint16_t* orow = out + ((size_t)m * ORC_NS * ORC_GS + hq) * ORC_DS;
+            for (int d = 0; d < ORC_DS; ++d) orow[d] = orc_bf16_rne(l > 0.0 ? (float)(o[d] / l) : 0.0f);
+        }
+}
+
 /* --------------------------------------------------------------------- FFN */
 
 /* One output row of a projection with the format's rounding rule. xf: f32 activation. */

@@ -87,6 +87,10 @@ void orc_sliding_project_qkv(const uint16_t* x, const uint8_t* q_w, const uint8_
 
 /* ops::sliding_attention_output, FO/src/ops.rs:130-146; oracle generate_references.py:337-355.
  * x [M,4096]; o_w [3840,4096]; residual [M,3840] updated in place. */
+/* ops::sliding_attention (FO/src/ops.rs:118-128): q, out [M][8][2][256] bf16; k, v [1024][8][256]
+ * bf16; mask [M][1024] f32 (slot t takes part when mask != 0). */
+void orc_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                           uint16_t* out, int M);
 void orc_sliding_attention_output(const uint16_t* x, const uint16_t* post_rms, const uint8_t* o_w,
                                   const float* o_s, uint16_t* residual, int M);
 

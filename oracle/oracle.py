@@ -72,6 +72,7 @@ def _declare(l: C.CDLL) -> None:
     l.orc_scaled_projection_fp8.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, P]
     l.orc_sliding_project_qkv.argtypes = [P] * 10 + [C.c_int32, C.c_int32] + [P] * 5 + [C.c_int]
     l.orc_sliding_attention_output.argtypes = [P, P, P, P, P, C.c_int]
+    l.orc_sliding_attention.argtypes = [P, P, P, P, P, C.c_int]
     l.orc_decoder_feedforward.argtypes = [P, P, P, P, P, C.c_int]
     l.orc_ffn_up_gate.argtypes = [P, P, P, C.c_int]
     l.orc_ffn_down.argtypes = [P, P, P, C.c_int]
@@ -229,6 +230,16 @@ def sliding_attention_output(x, post_rms, o_w, o_s, residual):
     lib().orc_sliding_attention_output(_p(x), _p(_u16(post_rms)), _p(np.ascontiguousarray(o_w)),
                                        _p(np.ascontiguousarray(o_s, dtype=np.float32)), _p(residual),
                                        x.shape[0])
+
+
+def sliding_attention(q, k, v, mask):
+    """ops::sliding_attention (FO/src/ops.rs:118-128). Returns out bf16 bits [M, 8, 2, 256]."""
+    q = _u16(q).reshape(-1, QS)
+    M = q.shape[0]
+    mask = np.ascontiguousarray(mask, dtype=np.float32).reshape(M, TS)
+    out = np.zeros((M, QS), np.uint16)
+    lib().orc_sliding_attention(_p(q), _p(_u16(k)), _p(_u16(v)), _p(mask), _p(out), M)
+    return out.reshape(M, NS, GS, DS)
 
 
 def ffn_weights(fmt: int, up, gate, down, up_s, gate_s, down_s, inv_g=(1.0, 1.0, 1.0)):
