@@ -49,7 +49,9 @@ MALL_BYTES = 256 << 20
 # Algorithmic bytes per call (weights + scales + operator-boundary vectors).
 BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          # sliding_attention, all 1024 slots valid: K and V caches + q + out + mask row
-         "attn": 2 * 1024 * 8 * 256 * 2 + 2 * 4096 * 2 + 1024 * 4}
+         "attn": 2 * 1024 * 8 * 256 * 2 + 2 * 4096 * 2 + 1024 * 4,
+         # final_norm_and_logits: the bf16 lm_head (262144 x 3840) + input + norm weight + logits
+         "logits": 262144 * 3840 * 2 + 2 * 3840 * 2 + 262144 * 2}
 GRAPH_CALLS = 40  # calls per captured graph
 # Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
 FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
@@ -68,7 +70,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
-    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "chunk"), default=None,
+    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "chunk"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     args = ap.parse_args()
@@ -111,6 +113,10 @@ def main() -> int:
     AW = replicate(att, ("k_cache", "v_cache"), na)
     a_q, a_mask = dev(att["q"]), dev(att["mask"])
     a_out = torch.zeros(4096, dtype=torch.int16, device="cuda")
+    # the lm_head (2 GB, one copy: it is 8x the MALL) is drawn on the device
+    lg = synth.cfg_logits(0)
+    lg_in, lg_rms, lg_w = dev(lg["input"]), dev(lg["rms_weight"]), synth.lm_head_device(0)
+    lg_out = torch.zeros(synth.W, dtype=torch.int16, device="cuda")
     f_res, f_pre, f_post, f_ls = (dev(ffn[k]) for k in ("residual", "pre_ff_rms_weight", "post_ff_rms_weight",
                                                           "layer_scalar"))
     o_x, o_post, o_res = dev(o["x"]), dev(o["post_attn_rms_weight"]), dev(o["residual"])
@@ -175,6 +181,9 @@ def main() -> int:
         w = AW[i % na]
         ops.sliding_attention(a_q, w["k_cache"], w["v_cache"], a_mask, a_out)
 
+    def run_logits(i):
+        ops.final_norm_and_logits(lg_in, lg_rms, lg_w, lg_out)
+
     def run_step(i):
         run_qkv(i)
         run_o(i)
@@ -216,7 +225,8 @@ def main() -> int:
         return a.elapsed_time(b) / (reps * GRAPH_CALLS), reps * GRAPH_CALLS
 
     if args.profile:
-        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "chunk": run_layer}[args.profile]
+        fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
+              "chunk": run_layer}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -229,7 +239,7 @@ def main() -> int:
         return 0
 
     per_op = {}
-    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn)):
+    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn), ("logits", run_logits)):
         ms, _ = graph_timed(fn, args.steps, args.warmup)
         ms_host = timed(fn, min(args.steps, 50), 5)
         gbps = BYTES[name] / (ms * 1e-3) / 1e9

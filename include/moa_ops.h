@@ -142,14 +142,21 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
                                   const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
                                   int M, void* stream);
 
+/* ops::final_norm_and_logits -- FO/src/ops.rs:241-298 (oracle gemma4.py:256-261).
+ * input bf16 [M,3840]; rms_weight bf16 [3840]; lm_head_weight bf16 [262144,3840]; out bf16
+ * [M,262144] = bf16(bf16(tanh(bf16(l / 30))) * 30), l = bf16(RMSNorm(input) . W_v). */
+int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight, const uint16_t* lm_head_weight,
+                              uint16_t* out, int M, void* stream);
+
 /* The FP8 projection alone -- FO/scripts/generate_references.py:265-274 scaled_projection:
  * out[m,n] = bf16((x[m,:] . dec(w[n,:])) * scale[n]). x bf16 [M,K], w E4M3 [N,K], scale f32
  * [N], out bf16 [M,N]; K % 16 == 0. */
 int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* scale, uint16_t* out,
                               int M, int N, int K, void* stream);
 
-/* Test support: decodes every E4M3 code, E2M1 byte, E8M0 code and bf16 GeLU input with the
- * kernels' own device helpers into out (device uint32 [66564]; layout in moa_decode.hip). */
+/* Test support: decodes every E4M3 code, E2M1 byte, E8M0 code, bf16 GeLU input and bf16
+ * final-logit softcap input with the kernels' own device helpers into out (device uint32
+ * [132100]; layout in moa_decode.hip). */
 int moa_format_selftest(uint32_t* out, void* stream);
 
 #ifdef __cplusplus

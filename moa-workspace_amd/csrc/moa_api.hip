@@ -325,6 +325,15 @@ int moa_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* 
                   "sliding_attention launch");
 }
 
+int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight, const uint16_t* lm_head_weight,
+                              uint16_t* out, int M, void* stream) {
+    Check c;
+    c.ptr(input, "input").ptr(rms_weight, "rms_weight").ptr(lm_head_weight, "lm_head_weight").ptr(out, "out").rows(M);
+    if (c.code) return c.code;
+    return finish(launch_final_norm_and_logits(input, rms_weight, lm_head_weight, out, M, static_cast<hipStream_t>(stream)),
+                  "final_norm_and_logits launch");
+}
+
 int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* scale, uint16_t* out,
                               int M, int N, int K, void* stream) {
     Check c;

@@ -1443,6 +1443,7 @@ __global__ __launch_bounds__(kBlock) void proj_decode_kernel(ProjParams p) {
 //   out[1024,66560)   bf16 bits of bf16(gelu_tanh(bf16 value i))
 //   out[66560,66564)  f32 bits of the first E2M1 value of byte 0x77 (6.0) converted with the
 //                     f32 scale 15, 2, 3, 0.75 -- records how the hardware applies the scale
+//   out[66564,132100) bf16 bits of the final-logit softcap of bf16 value i
 __global__ void format_selftest_kernel(uint32_t* out) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < 4) {
@@ -1461,7 +1462,10 @@ __global__ void format_selftest_kernel(uint32_t* out) {
         out[256 + 2 * i + 1] = __float_as_uint(w[1]);
         out[768 + i] = __float_as_uint(e8m0_to_f32((uint32_t)i));
     }
-    if (i < 65536) out[1024 + i] = f2bf(gelu_tanh(bf2f((uint32_t)i)));
+    if (i < 65536) {
+        out[1024 + i] = f2bf(gelu_tanh(bf2f((uint32_t)i)));
+        out[66564 + i] = softcap30_bf16(bf2f((uint32_t)i));
+    }
 }
 
 template <typename K, typename... A>

@@ -124,23 +124,47 @@ __device__ __forceinline__ float rms_inverse(float sum_sq, int n) {
     return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, kEps)));
 }
 
-// torch gelu(approximate="tanh") in f32 (gemma4.py:197): 0.5*x*(1+tanh(sqrt(2/pi)*(x+0.044715*x^3))).
-// gelu(approximate="tanh") = 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3)
-// (gemma4.py:197). tanh(u) = sign(u) (1 - 2 / (1 + e^(2|u|))): e^(2|u|) = 2^(2|u| log2 e) from
-// v_exp_f32, 1 / (1 + e^(2|u|)) from v_rcp_f32 refined by one Newton step (r + r (1 - d r)), and
-// no branches (a library tanhf branches on |u|, which serialises element-wise loops). For |u|
-// beyond ~9 the quotient vanishes next to 1, so 1 + tanh(u) is exactly 0 or 2 as in f32 tanhf.
-// Over all 65536 bf16 inputs it rounds to the same bf16 as the f32 formula with libm tanhf.
+// tanh(u) = sign(u) (1 - 2 / (1 + e^(2|u|))) in f32 without branches: e^(2|u|) = 2^(2|u| log2 e)
+// from v_exp_f32, 1 / (1 + e^(2|u|)) from v_rcp_f32 refined by one Newton step (r + r (1 - d r)).
+// A library tanhf branches on |u|, which serialises element-wise loops. For |u| beyond ~9 the
+// quotient vanishes next to 1, so the result is exactly +-1 as with f32 tanhf.
+__device__ __forceinline__ float tanh_f32(float u) {
+    const float d = 1.0f + __builtin_amdgcn_exp2f(fabsf(u) * 2.8853900817779268f);
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    const float r = __builtin_isinf(d) ? 0.0f : fmaf(r0, fmaf(-d, r0, 1.0f), r0);
+    return copysignf(1.0f - 2.0f * r, u);
+}
+
+// torch gelu(approximate="tanh") in f32 (gemma4.py:197): 0.5 x (1 + tanh(u)),
+// u = sqrt(2/pi) (x + 0.044715 x^3). Over all 65536 bf16 inputs it rounds to the same bf16 as
+// the f32 formula with libm tanhf.
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float kBeta = 0.7978845608028654f;
     const float kKappa = 0.044715f;
     const float cube = x * x * x;
     const float inner = kBeta * (x + kKappa * cube);
-    const float d = 1.0f + __builtin_amdgcn_exp2f(fabsf(inner) * 2.8853900817779268f);
-    const float r0 = __builtin_amdgcn_rcpf(d);
-    const float r = __builtin_isinf(d) ? 0.0f : fmaf(r0, fmaf(-d, r0, 1.0f), r0);
-    const float th = copysignf(1.0f - 2.0f * r, inner);
-    return 0.5f * x * (1.0f + th);
+    return 0.5f * x * (1.0f + tanh_f32(inner));
+}
+
+// tanh with a small relative error over the whole range: for |u| < 0.25 the odd Taylor series to
+// u^11 (truncation below 3e-10 relative), elsewhere tanh_f32, whose 1 - 2 / d loses at most about
+// 1e-7 absolute, 5e-7 relative at |u| = 0.25. Both are evaluated; the select is branch-free.
+__device__ __forceinline__ float tanh_rel_f32(float u) {
+    const float u2 = u * u;
+    float p = fmaf(u2, -8.8632355299021966e-3f, 2.1869488536155203e-2f);  // -1382/155925, 62/2835
+    p = fmaf(u2, p, -5.3968253968253968e-2f);                              // -17/315
+    p = fmaf(u2, p, 1.3333333333333333e-1f);                               // 2/15
+    p = fmaf(u2, p, -3.3333333333333333e-1f);                              // -1/3
+    p = fmaf(u2 * u, p, u);
+    return fabsf(u) < 0.25f ? p : tanh_f32(u);
+}
+
+// Gemma's final-logit softcap on a bf16 logit l (FO/src/ops.rs:256-293): l is widened to f32,
+// divided by 30, tanh'd, multiplied by 30 and rounded once to bf16. (The torch CPU model,
+// gemma4.py:260-261, rounds to bf16 after each of the three ops; the two differ by at most a
+// couple of bf16 ulps.)
+__device__ __forceinline__ uint32_t softcap30_bf16(float l) {
+    return f2bf(tanh_rel_f32(l / 30.0f) * 30.0f);
 }
 
 }  // namespace moa

@@ -118,6 +118,10 @@ hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, De
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);  // FP8 weights
 
+// ops::final_norm_and_logits for M token rows (input [M][kH], out [M][kW]).
+hipError_t launch_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_w, const uint16_t* w, uint16_t* out,
+                                        int M, hipStream_t s);
+
 // ops::sliding_attention for M token rows (q / out [M][kNs][kGs][kDs], mask [M][kTs]).
 hipError_t launch_sliding_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const float* mask,
                                     uint16_t* out, int M, hipStream_t s, DevCtx* ctx);

@@ -11,5 +11,6 @@ constexpr int kQs = 4096;   // kNs * kGs * kDs
 constexpr int kPs = 2048;   // kNs * kDs
 constexpr int kTs = 1024;   // ring-cache slots
 constexpr int kE = 32768;   // RoPE table rows
+constexpr int kW = 262144;  // vocabulary rows of lm_head (FO/src/axes.rs: W)
 constexpr float kEps = 1e-6f;
 }  // namespace moa

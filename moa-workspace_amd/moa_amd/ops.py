@@ -19,7 +19,7 @@ import torch
 
 from . import _lib
 
-H, L, NS, GS, DS, QS, PS, TS, E = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768
+H, L, NS, GS, DS, QS, PS, TS, E, W = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768, 262144
 
 
 def _ptr(t: torch.Tensor | None, name: str, dtypes, numel: int | None = None):
@@ -93,6 +93,17 @@ def sliding_attention(q, k, v, mask, out) -> None:
         _ptr(mask, "mask", _F32, M * TS), _ptr(out, "out", _BF16, M * QS),
     ]
     _lib.call("moa_sliding_attention", *args, M, _stream(q))
+
+
+def final_norm_and_logits(input, rms_weight, lm_head_weight, out) -> None:
+    """ops::final_norm_and_logits (FO/src/ops.rs:241-298): out = softcap30(bf16(RMSNorm(input) .
+    lm_head_weight^T)). input [M, 3840] bf16, lm_head_weight [262144, 3840] bf16, out [M, 262144] bf16."""
+    M = _rows(input, H, "input")
+    args = [
+        _ptr(input, "input", _BF16), _ptr(rms_weight, "rms_weight", _BF16, H),
+        _ptr(lm_head_weight, "lm_head_weight", _BF16, W * H), _ptr(out, "out", _BF16, M * W),
+    ]
+    _lib.call("moa_final_norm_and_logits", *args, M, _stream(input))
 
 
 def sliding_attention_output(x, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
@@ -178,7 +189,7 @@ def device_errors(device: torch.device | None = None) -> int:
 
 
 def format_selftest(device="cuda") -> torch.Tensor:
-    out = torch.zeros(66564, dtype=torch.int32, device=device)  # layout: moa_decode.hip format_selftest_kernel
+    out = torch.zeros(132100, dtype=torch.int32, device=device)  # layout: moa_decode.hip format_selftest_kernel
     _lib.call("moa_format_selftest", C.c_void_p(out.data_ptr()), _stream(out))
     return out
 

@@ -14,7 +14,7 @@ import numpy as np
 from . import formats as F
 from . import prng
 
-H, L, NS, GS, DS, QS, PS, TS, E = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768
+H, L, NS, GS, DS, QS, PS, TS, E, W = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768, 262144
 
 # Reference distributions (test_kernels.rs:147-155; generate_references.py:64-77).
 WEIGHT_EXP = (7, 14)
@@ -240,6 +240,41 @@ def cfg_attention(seed: int = 0, M: int = 1, pos=1023, q_std: float = 1.0, tag: 
     return dict(q=bf16_normal(n("q"), (M, NS, QS // (NS * DS), DS), q_std),
                 k_cache=bf16_normal(n("k_cache"), (TS, NS, DS)), v_cache=bf16_normal(n("v_cache"), (TS, NS, DS)),
                 mask=attention_mask(M, pos))
+
+
+def lm_head_bits(r):
+    """bf16 lm_head values from random integers r in [0, 65536) (numpy or torch int32): the sign and
+    mantissa bits of r, exponent 2^-5 .. 2^-2 from two more bits, so |w| lies in [1/32, 1/2) with an
+    RMS of ~0.22. A unit-RMS input row then gives logits of std ~14, which spans the softcap's curve."""
+    return (r & 0x807F) | ((122 + ((r >> 7) & 3)) << 7)
+
+
+def cfg_logits(seed: int = 0, M: int = 1, tag: str = "logits") -> dict:
+    """final_norm_and_logits inputs without the lm_head: input [M, 3840] ~ N(0, 1), the final norm's
+    weight. The [262144, 3840] lm_head (2 GB) comes from lm_head_device or lm_head_rows."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    return dict(input=bf16_normal(n("input"), (M, H)), rms_weight=rms_weight(n("rms"), H))
+
+
+def lm_head_rows(seed: int, rows: int, tag: str = "logits") -> np.ndarray:
+    """A host lm_head of `rows` vocabulary rows (bf16 bits [rows, 3840]), for CPU-sized checks."""
+    r = _gen(f"{tag}.seed{seed}.lm_head").integers(0, 1 << 16, size=(rows, H), dtype=np.int32)
+    return lm_head_bits(r).astype(np.uint16)
+
+
+def lm_head_device(seed: int, device="cuda"):
+    """The full [262144, 3840] lm_head, drawn on the device (torch's generator; host generation of
+    2 GB takes a minute), as an int16 tensor of bf16 bits."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    out = torch.empty((W, H), dtype=torch.int16, device=device)
+    step = 16384
+    for r0 in range(0, W, step):
+        r = torch.randint(0, 1 << 16, (step, H), dtype=torch.int32, device=device, generator=g)
+        b = lm_head_bits(r)
+        out[r0:r0 + step] = torch.where(b >= 32768, b - 65536, b).to(torch.int16)
+    return out
 
 
 def cfg_ffn_mxfp4(seed: int = 0, M: int = 1, tag: str = "cfg3") -> dict:

@@ -385,6 +385,41 @@ void orc_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t*
         }
 }
 
+/* ------------------------------------------------------------------ logits */
+
+/* f64 -> bf16 with one rounding (to nearest even). The f32 step can only land on a bf16 tie that
+ * the f64 value does not sit on; such a tie is moved one f32 step toward the f64 value first. */
+static uint16_t bf16_rne_f64(double d) {
+    float f = (float)d;
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if (isfinite(f) && (u & 0xffffu) == 0x8000u && (double)f != d) f = nextafterf(f, d > (double)f ? INFINITY : -INFINITY);
+    return orc_bf16_rne(f);
+}
+
+uint16_t orc_softcap30(uint16_t l) {
+    const double v = orc_bf16_to_f32(l);
+    return bf16_rne_f64(tanh(v / 30.0) * 30.0);
+}
+
+void orc_final_norm_and_logits(const uint16_t* x, const uint16_t* rms_w, const uint16_t* lm_head, int W,
+                               uint16_t* out, int M) {
+    for (int m = 0; m < M; ++m) {
+        uint16_t h[ORC_H];
+        float hf[ORC_H];
+        orc_rmsnorm_row(x + (size_t)m * ORC_H, rms_w, ORC_H, h);
+        for (int i = 0; i < ORC_H; ++i) hf[i] = orc_bf16_to_f32(h[i]);
+#pragma omp parallel for schedule(static)
+        for (int r = 0; r < W; ++r) {
+            const uint16_t* wr = lm_head + (size_t)r * ORC_H;
+            double acc[LANES] = {0};
+            for (int k = 0; k < ORC_H; ++k) acc[k % LANES] += (double)hf[k] * orc_bf16_to_f32(wr[k]);
+            /* the lm_head linear's bf16 output feeds the softcap */
+            out[(size_t)m * W + r] = orc_softcap30(orc_bf16_rne(reduce_lanes(acc)));
+        }
+    }
+}
+
 /* --------------------------------------------------------------------- FFN */
 
 /* One output row of a projection with the format's rounding rule. xf: f32 activation. */

@@ -85,14 +85,23 @@ void orc_sliding_project_qkv(const uint16_t* x, const uint8_t* q_w, const uint8_
                              const uint16_t* cos_tab, const uint16_t* sin_tab,
                              uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M);
 
-/* ops::sliding_attention_output, FO/src/ops.rs:130-146; oracle generate_references.py:337-355.
- * x [M,4096]; o_w [3840,4096]; residual [M,3840] updated in place. */
 /* ops::sliding_attention (FO/src/ops.rs:118-128): q, out [M][8][2][256] bf16; k, v [1024][8][256]
  * bf16; mask [M][1024] f32 (slot t takes part when mask != 0). */
 void orc_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
                            uint16_t* out, int M);
+/* ops::sliding_attention_output, FO/src/ops.rs:130-146; oracle generate_references.py:337-355.
+ * x [M,4096]; o_w [3840,4096]; residual [M,3840] updated in place. */
 void orc_sliding_attention_output(const uint16_t* x, const uint16_t* post_rms, const uint8_t* o_w,
                                   const float* o_s, uint16_t* residual, int M);
+
+/* Gemma's final-logit softcap of a bf16 logit l (FO/src/ops.rs:256-293; gemma4.py:260-261):
+ * tanh(l / 30) * 30 in f64, rounded once to bf16. */
+uint16_t orc_softcap30(uint16_t l);
+/* ops::final_norm_and_logits (FO/src/ops.rs:241-298): RMSNorm of each input row, the bf16 linear
+ * over the W rows of lm_head given ([W][3840], any run of vocabulary rows), then the softcap.
+ * x [M][3840]; out [M][W]. */
+void orc_final_norm_and_logits(const uint16_t* x, const uint16_t* rms_w, const uint16_t* lm_head, int W,
+                               uint16_t* out, int M);
 
 /* ops::decoder_feedforward, FO/src/ops.rs:201-239; oracle generate_references.py:375-414.
  * Weight format selects the projection rule:

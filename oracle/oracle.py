@@ -16,7 +16,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 
-H, L, NS, GS, DS, QS, PS, TS, E = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768
+H, L, NS, GS, DS, QS, PS, TS, E, W = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768, 262144
 FFN_NVFP4, FFN_FP8, FFN_MXFP4 = 0, 1, 2
 
 _lib = None
@@ -73,6 +73,9 @@ def _declare(l: C.CDLL) -> None:
     l.orc_sliding_project_qkv.argtypes = [P] * 10 + [C.c_int32, C.c_int32] + [P] * 5 + [C.c_int]
     l.orc_sliding_attention_output.argtypes = [P, P, P, P, P, C.c_int]
     l.orc_sliding_attention.argtypes = [P, P, P, P, P, C.c_int]
+    l.orc_softcap30.argtypes = [C.c_uint16]
+    l.orc_softcap30.restype = C.c_uint16
+    l.orc_final_norm_and_logits.argtypes = [P, P, P, C.c_int, P, C.c_int]
     l.orc_decoder_feedforward.argtypes = [P, P, P, P, P, C.c_int]
     l.orc_ffn_up_gate.argtypes = [P, P, P, C.c_int]
     l.orc_ffn_down.argtypes = [P, P, P, C.c_int]
@@ -240,6 +243,21 @@ def sliding_attention(q, k, v, mask):
     out = np.zeros((M, QS), np.uint16)
     lib().orc_sliding_attention(_p(q), _p(_u16(k)), _p(_u16(v)), _p(mask), _p(out), M)
     return out.reshape(M, NS, GS, DS)
+
+
+def softcap30(l: int) -> int:
+    """Gemma's final-logit softcap of one bf16 logit (FO/src/ops.rs:256-293), bf16 bits."""
+    return int(lib().orc_softcap30(int(l)))
+
+
+def final_norm_and_logits(x, rms_w, lm_head_rows):
+    """ops::final_norm_and_logits (FO/src/ops.rs:241-298) over the vocabulary rows given
+    (lm_head_rows [W, 3840] bf16, any subset). Returns out bf16 bits [M, W]."""
+    x = _u16(x).reshape(-1, H)
+    w = _u16(lm_head_rows).reshape(-1, H)
+    out = np.zeros((x.shape[0], w.shape[0]), np.uint16)
+    lib().orc_final_norm_and_logits(_p(x), _p(_u16(rms_w)), _p(w), w.shape[0], _p(out), x.shape[0])
+    return out
 
 
 def ffn_weights(fmt: int, up, gate, down, up_s, gate_s, down_s, inv_g=(1.0, 1.0, 1.0)):
