@@ -31,6 +31,8 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 }  // namespace
 
+int set_error(int code, const char* msg) { return fail(code, msg); }
+
 DevCtx* device_context(hipError_t* err) {
     int dev = 0;
     *err = hipGetDevice(&dev);

@@ -77,6 +77,9 @@ struct DevCtx {
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
 DevCtx* device_context(hipError_t* err);
 
+// Records `msg` as this thread's last error (moa_last_error_string) and returns `code`.
+int set_error(int code, const char* msg);
+
 enum class ScaleKind { F32, BF16 };
 enum class FfnFormat { FP8, NVFP4, MXFP4 };
 

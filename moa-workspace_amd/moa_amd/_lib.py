@@ -1,4 +1,4 @@
-"""ctypes binding of libmoa_gfx950.so (declarations mirror include/moa_ops.h).
+"""ctypes binding of libmoa_gfx950.so (declarations mirror include/moa_ops.h and include/moa_ckpt.h).
 
 Loading fails loudly when the library is missing: there is no CPU fallback.
 """
@@ -18,6 +18,9 @@ ERRORS = {
     -3: "MOA_ERROR_HIP",
     -4: "MOA_ERROR_NO_DEVICE",
     -5: "MOA_ERROR_DEVICE_STATE",
+    -6: "MOA_ERROR_NOT_FOUND",
+    -7: "MOA_ERROR_FORMAT",
+    -8: "MOA_ERROR_IO",
 }
 DEVERR_ROPE_OFFSET = 1
 DEVERR_KV_OFFSET = 2
@@ -31,12 +34,27 @@ class MoaError(RuntimeError):
 
 
 P, I32, U32P = C.c_void_p, C.c_int, C.POINTER(C.c_uint32)
+S, I64, U64 = C.c_char_p, C.c_int64, C.c_uint64
 
 # name -> argtypes (restype is int unless listed in _RESTYPES)
 SIGNATURES = {
     "moa_version": [],
     "moa_last_error_string": [],
     "moa_init": [I32],
+    # include/moa_ckpt.h
+    "moa_ckpt_open": [S, C.POINTER(P)],
+    "moa_ckpt_close": [P],
+    "moa_ckpt_count": [P, C.POINTER(C.c_int)],
+    "moa_ckpt_name": [P, I32, C.POINTER(S)],
+    "moa_ckpt_info": [P, S, C.POINTER(S), C.POINTER(I64), C.POINTER(C.c_int), C.POINTER(U64)],
+    "moa_ckpt_read": [P, S, P, U64],
+    "moa_ckpt_load_bf16": [P, S, C.POINTER(I64), I32, P, P],
+    "moa_ckpt_load_bf16_column": [P, S, I64, P, P],
+    "moa_ckpt_load_f8": [P, S, I64, I64, P, P],
+    "moa_ckpt_load_f4": [P, S, I64, I64, P, P],
+    "moa_ckpt_load_scalar_bf16": [P, S, P, P],
+    "moa_ckpt_global_scale": [P, S, C.POINTER(C.c_float)],
+    "moa_ckpt_load_global_scale": [P, S, P, P],
     "moa_device_errors": [P, U32P],
     "moa_sliding_project_qkv": [P] * 17 + [I32, P],
     "moa_sliding_project_qkv_bf16_scales": [P] * 17 + [I32, P],

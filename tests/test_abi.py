@@ -1,4 +1,4 @@
-"""The C ABI library: loads, exports every symbol include/moa_ops.h declares, and rejects bad
+"""The C ABI library: loads, exports every symbol include/*.h declares, and rejects bad
 arguments on the host before touching a device (no compute calls here)."""
 import ctypes as C
 import re
@@ -12,9 +12,11 @@ ROOT = Path(__file__).resolve().parent.parent
 
 
 def header_functions():
-    text = (ROOT / "include" / "moa_ops.h").read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(moa_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(moa_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_builds_and_loads():
