@@ -144,7 +144,43 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
 
 /* ops::final_norm_and_logits -- FO/src/ops.rs:241-298 (oracle gemma4.py:256-261).
  * input bf16 [M,3840]; rms_weight bf16 [3840]; lm_head_weight bf16 [262144,3840]; out bf16
- * [M,262144] = bf16(bf16(tanh(bf16(l / 30))) * 30), l = bf16(RMSNorm(input) . W_v). */
+ * [M,262144] = bf16(tanh(l / 30) * 30) in f32, l = bf16(RMSNorm(input) . W_v). */
+/* ---- full-attention layers (every sixth layer): 16 query heads and one KV head of 512, a
+ * cache of 512-slot pages (FO/src/axes.rs: Gf=16, Df=512, Qf=8192, Pf=512, Tf=512). ---- */
+
+/* ops::full_project_qkv -- FO/src/ops.rs:78-116 (oracle gemma4.py:152-166, attention_k_eq_v).
+ * x bf16 [M,3840]; q_weight E4M3 [8192,3840], k_weight E4M3 [512,3840] with bf16 per-row
+ * scales; q_rms_weight, k_rms_weight bf16 [512]; cos/sin bf16 [32768,512] (sin's low half
+ * negated). Row m: q_out[m] = RoPE(RMSNorm_q(q)) [16,512]; of the raw K projection, the page's
+ * slot kv_offset/1024 + m gets K = RoPE(RMSNorm_k(k)) in k_cache [512,512] and the unweighted
+ * norm V = RMSNorm(k) in v_cache [512,512]. RoPE row rope_offset/1024 + m. A row whose slot
+ * falls past the page writes nothing and raises MOA_DEVERR_KV_OFFSET. */
+int moa_full_project_qkv(const uint16_t* x, const uint8_t* q_weight, const uint8_t* k_weight,
+                         const uint16_t* q_weight_scale, const uint16_t* k_weight_scale,
+                         const uint16_t* input_rms_weight, const uint16_t* q_rms_weight, const uint16_t* k_rms_weight,
+                         const int32_t* kv_offset, const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
+                         uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M, void* stream);
+
+/* ops::full_attention_first_page / ops::full_attention_page -- FO/src/ops.rs:148-174
+ * (FO/src/device/full/attention.rs:203-329). q bf16 [M,16,512]; one page's k, v bf16 [512,512];
+ * mask f32 [M,512] (slot t takes part when non-zero); the running state running_max,
+ * running_sum f32 [M,16] and out bf16 [M,16,512] (un-normalised: sum of exp(s - max) v).
+ * first_page starts the state from this page; page folds this page into it (the old state is
+ * rescaled by exp(old max - new max)). Scores use scale 1.0. A head with no valid slot so far
+ * has max -inf, sum 0 and out 0. */
+int moa_full_attention_first_page(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                                  float* running_max, float* running_sum, uint16_t* out, int M, void* stream);
+int moa_full_attention_page(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                            float* running_max, float* running_sum, uint16_t* out, int M, void* stream);
+
+/* ops::full_attention_output -- FO/src/ops.rs:176-199. x bf16 [M,16,512] (the pages' out),
+ * running_sum f32 [M,16]; residual bf16 [M,3840] updated in place:
+ * r = bf16(r + RMSNorm(bf16(bf16(x / sum) . W_o) * s)) with o_weight E4M3 [3840,8192] and bf16
+ * per-row scales (a zero sum gives a zero attention row). */
+int moa_full_attention_output(const uint16_t* x, const float* running_sum, const uint16_t* post_attn_rms_weight,
+                              const uint8_t* o_weight, const uint16_t* o_weight_scale, uint16_t* residual, int M,
+                              void* stream);
+
 int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight, const uint16_t* lm_head_weight,
                               uint16_t* out, int M, void* stream);
 

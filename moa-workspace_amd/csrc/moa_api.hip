@@ -58,6 +58,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
     const size_t t_ptag = carve(sizeof(uint64_t) * (kL / 2));
     const size_t t_attn = carve(sizeof(float) * kAttnPartFloats);
+    const size_t t_fattn = carve(sizeof(float) * kFattnPartFloats);
     int cus = 0;
     *err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (*err != hipSuccess) return nullptr;
@@ -85,6 +86,7 @@ DevCtx* device_context(hipError_t* err) {
     c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
     c.ffn_ptag = reinterpret_cast<uint64_t*>(b + t_ptag);
     c.attn_part = reinterpret_cast<float*>(b + t_attn);
+    c.fattn_part = reinterpret_cast<float*>(b + t_fattn);
     c.base = base;
     return &c;
 }
@@ -325,6 +327,64 @@ int moa_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* 
     if (!ctx) return code;
     return finish(launch_sliding_attention(q, k, v, mask, out, M, static_cast<hipStream_t>(stream), ctx),
                   "sliding_attention launch");
+}
+
+int moa_full_project_qkv(const uint16_t* x, const uint8_t* q_weight, const uint8_t* k_weight,
+                         const uint16_t* q_weight_scale, const uint16_t* k_weight_scale,
+                         const uint16_t* input_rms_weight, const uint16_t* q_rms_weight, const uint16_t* k_rms_weight,
+                         const int32_t* kv_offset, const int32_t* rope_offset, const uint16_t* cos, const uint16_t* sin,
+                         uint16_t* k_cache, uint16_t* v_cache, uint16_t* q_out, int M, void* stream) {
+    Check c;
+    c.ptr(x, "x").ptr(q_weight, "q_weight").ptr(k_weight, "k_weight");
+    c.ptr(q_weight_scale, "q_weight_scale", 2).ptr(k_weight_scale, "k_weight_scale", 2);
+    c.ptr(input_rms_weight, "input_rms_weight").ptr(q_rms_weight, "q_rms_weight").ptr(k_rms_weight, "k_rms_weight");
+    c.ptr(kv_offset, "kv_offset", 4).ptr(rope_offset, "rope_offset", 4).ptr(cos, "cos").ptr(sin, "sin");
+    c.ptr(k_cache, "k_cache").ptr(v_cache, "v_cache").ptr(q_out, "q_out").rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    QkvParams p{x, q_weight, k_weight, nullptr, q_weight_scale, k_weight_scale, nullptr, ScaleKind::BF16,
+                input_rms_weight, q_rms_weight, k_rms_weight, kv_offset, rope_offset, cos, sin, k_cache, v_cache, q_out};
+    return finish(launch_full_qkv(p, M, static_cast<hipStream_t>(stream), ctx), "full_project_qkv launch");
+}
+
+static int full_page(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask, float* running_max,
+                     float* running_sum, uint16_t* out, int M, bool first, void* stream) {
+    Check c;
+    c.ptr(q, "q").ptr(k, "k").ptr(v, "v").ptr(mask, "mask", 4).ptr(running_max, "running_max", 4);
+    c.ptr(running_sum, "running_sum", 4).ptr(out, "out").rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return finish(launch_full_attention_page(q, k, v, mask, running_max, running_sum, out, M, first,
+                                             static_cast<hipStream_t>(stream), ctx),
+                  first ? "full_attention_first_page launch" : "full_attention_page launch");
+}
+
+int moa_full_attention_first_page(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                                  float* running_max, float* running_sum, uint16_t* out, int M, void* stream) {
+    return full_page(q, k, v, mask, running_max, running_sum, out, M, true, stream);
+}
+
+int moa_full_attention_page(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
+                            float* running_max, float* running_sum, uint16_t* out, int M, void* stream) {
+    return full_page(q, k, v, mask, running_max, running_sum, out, M, false, stream);
+}
+
+int moa_full_attention_output(const uint16_t* x, const float* running_sum, const uint16_t* post_attn_rms_weight,
+                              const uint8_t* o_weight, const uint16_t* o_weight_scale, uint16_t* residual, int M,
+                              void* stream) {
+    Check c;
+    c.ptr(x, "x").ptr(running_sum, "running_sum", 4).ptr(post_attn_rms_weight, "post_attn_rms_weight");
+    c.ptr(o_weight, "o_weight").ptr(o_weight_scale, "o_weight_scale", 2).ptr(residual, "residual").rows(M);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    OParams p{x, post_attn_rms_weight, o_weight, o_weight_scale, ScaleKind::BF16, residual, running_sum};
+    return finish(launch_full_o(p, M, static_cast<hipStream_t>(stream), ctx), "full_attention_output launch");
 }
 
 int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight, const uint16_t* lm_head_weight,

@@ -595,7 +595,52 @@ __device__ __forceinline__ void qkv_head_epilogue(const QkvParams& p, const uint
     dst[t] = (uint16_t)f2bf(a + b);
 }
 
-template <ScaleKind SK>
+// ------------------------------------------------------------ QKV of a full-attention layer
+// ops::full_project_qkv (FO/src/ops.rs:78-116): 8704 projection rows (Q 8192 | K 512), K = 3840.
+// The one KV head's raw projection gives K (weighted RMSNorm over 512, RoPE) and V (unweighted
+// RMSNorm) -- the CPU reference's attention_k_eq_v path (gemma4.py:152-166; full/rmsnorm.rs).
+// The slot is kv_offset / 1024 + m of the caller's page: a row whose slot falls past the page's
+// 512 slots writes nothing and raises the kv-offset error bit.
+constexpr int kFqkvRows = kQf + kPf;
+
+// Per-head epilogue by the head's last workgroup: thread t owns head elements t and t + 256,
+// which are each other's RoPE partners.
+__device__ __forceinline__ void fqkv_head_epilogue(const QkvParams& p, const uint16_t* __restrict__ raw, int head,
+                                                   int m, uint32_t* err) {
+    __shared__ float red[4];
+    const int t = threadIdx.x;
+    constexpr int Hf = kDf / 2;
+    const int32_t rope_off = *p.rope_off;
+    const int32_t kv_off = *p.kv_off;
+    const bool rope_ok = rope_off >= 0 && (rope_off % (kDf * 2)) == 0 && rope_off / (kDf * 2) + m < kE;
+    const bool kv_ok = kv_off >= 0 && (kv_off % (kDf * 2)) == 0 && kv_off / (kDf * 2) + m < kTf;
+    if (!rope_ok || !kv_ok) {  // the row writes nothing (no q_out, K or V)
+        if (t == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
+        return;
+    }
+    const int slot = kv_off / (kDf * 2) + m;
+    const int trow = rope_off / (kDf * 2) + m;
+    const uint16_t* wn = head < kGf ? p.q_rms : p.k_rms;
+    const float w0 = bf2f(wn[t]), w1 = bf2f(wn[t + Hf]);
+    const float c0 = bf2f(p.cos[(size_t)trow * kDf + t]), c1 = bf2f(p.cos[(size_t)trow * kDf + t + Hf]);
+    const float s0 = bf2f(p.sin[(size_t)trow * kDf + t]), s1 = bf2f(p.sin[(size_t)trow * kDf + t + Hf]);
+    const float v0 = bf2f(collect(&raw[head * kDf + t])), v1 = bf2f(collect(&raw[head * kDf + t + Hf]));
+    const float inv = rms_inverse(block_sum(v0 * v0 + v1 * v1, red), kDf);  // squares of bf16 are exact
+    const float u0 = v0 * inv, u1 = v1 * inv;
+    if (head == kGf) {  // V: the unweighted norm (full/rmsnorm.rs normalize_value)
+        p.v_cache[(size_t)slot * kDf + t] = (uint16_t)f2bf(u0);
+        p.v_cache[(size_t)slot * kDf + t + Hf] = (uint16_t)f2bf(u1);
+    }
+    const float n0 = rbf(u0 * w0), n1 = rbf(u1 * w1);
+    // y = bf16(bf16(x*cos) + bf16(x_swap*sin_dev)); the table's sin has its low half negated
+    uint16_t* dst = head < kGf ? p.q_out + (size_t)m * kQf + head * kDf : p.k_cache + (size_t)slot * kDf;
+    dst[t] = (uint16_t)f2bf(rbf(n0 * c0) + rbf(n1 * s0));
+    dst[t + Hf] = (uint16_t)f2bf(rbf(n1 * c1) + rbf(n0 * s1));
+}
+
+// Full: false -- sliding_project_qkv (32 heads of 256); true -- full_project_qkv (17 heads of 512;
+// raw_all rows are kFqkvRows wide).
+template <ScaleKind SK, bool Full>
 __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0, uint16_t* raw_all,
                                                             uint32_t* tickets, uint32_t* err) {
     __shared__ float hs[kH];
@@ -607,9 +652,14 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
     const uint8_t* W;
     const void* S;
     int lr;
-    if (row0 < kQs) { W = p.qw; S = p.qs; lr = row0; }
-    else if (row0 < kQs + kPs) { W = p.kw; S = p.ks; lr = row0 - kQs; }
-    else { W = p.vw; S = p.vs; lr = row0 - kQs - kPs; }
+    if constexpr (Full) {
+        if (row0 < kQf) { W = p.qw; S = p.qs; lr = row0; }
+        else { W = p.kw; S = p.ks; lr = row0 - kQf; }
+    } else {
+        if (row0 < kQs) { W = p.qw; S = p.qs; lr = row0; }
+        else if (row0 < kQs + kPs) { W = p.kw; S = p.ks; lr = row0 - kQs; }
+        else { W = p.vw; S = p.vs; lr = row0 - kQs - kPs; }
+    }
 
     const float my_scale = load_scale<SK>(S, lr + min(lane, R - 1));  // lane r: row r's scale
     RmsStage st;
@@ -645,12 +695,15 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
         const float d = wave_sum(acc[r]);
         if (lane == r) mine = d;
     }
-    uint16_t* raw = raw_all + (size_t)m * kQkvRows;
+    constexpr int D = Full ? kDf : kDs;
+    uint16_t* raw = raw_all + (size_t)m * (Full ? kFqkvRows : kQkvRows);
     if (lane < R) publish(&raw[row0 + lane], f2bf(mine * my_scale));
 
-    const int head = row0 / kDs;  // 0..15 q, 16..23 k, 24..31 v (uniform over the block)
-    if (!block_arrive(&tickets[(kTicketQkv + m * 32 + head) * kTicketStride], kDs / (4 * R))) return;
-    qkv_head_epilogue(p, raw, head, m0 + m, err);
+    // sliding: 0..15 q, 16..23 k, 24..31 v; full: 0..15 q, 16 k (uniform over the block)
+    const int head = row0 / D;
+    if (!block_arrive(&tickets[(kTicketQkv + m * 32 + head) * kTicketStride], D / (4 * R))) return;
+    if constexpr (Full) fqkv_head_epilogue(p, raw, head, m0 + m, err);
+    else qkv_head_epilogue(p, raw, head, m0 + m, err);
 }
 
 // ------------------------------------------------------------ QKV: single launch (one token row)
@@ -828,24 +881,45 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
 // wave, 8 per workgroup, 480 workgroups per token row.
 constexpr int kOR = 2;
 
-template <ScaleKind SK>
+// The attention row as the O projection reads it. Sliding layers: x itself. Full-attention layers
+// (KX = kQf; div = the running softmax sums [16] of the row): x divided by its head's sum and
+// rounded to bf16, as full_attention_output does before projecting (full/attention.rs
+// divide_by_softmax_sum). A head with a zero sum (no valid slot) gives zeros.
+__device__ __forceinline__ uint4 o_input_chunk(uint4 v, const float* div, int k) {
+    const float d = div[k / kDf];
+    float f[8];
+    bf16x8_to_f32(v, f);
+    uint32_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        h[i] = f2bf(d > 0.0f ? f[2 * i] / d : 0.0f) | (f2bf(d > 0.0f ? f[2 * i + 1] / d : 0.0f) << 16);
+    return make_uint4(h[0], h[1], h[2], h[3]);
+}
+
+template <ScaleKind SK, int KX>
 __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uint16_t* pbuf_all,
                                                           uint32_t* tickets) {
-    __shared__ float xs[kQs];
-    constexpr int R = kOR, KI = kQs / 1024;
+    __shared__ float xs[KX];
+    constexpr int R = kOR, KI = KX / 1024;
     const int m = blockIdx.y;
     const int lane = lane_id(), wave = wave_id();
     const int row0 = blockIdx.x * (4 * R) + wave * R;
 
     const float my_scale = load_scale<SK>(p.os, row0 + min(lane, R - 1));
-    RowStage<kQs / 8> st;
-    row_issue(st, p.x + (size_t)(m0 + m) * kQs);
+    RowStage<KX / 8> st;
+    row_issue(st, p.x + (size_t)(m0 + m) * KX);
     uint4 wq[R][KI];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * kQs + j * 1024 + lane * 16);
+        for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * KX + j * 1024 + lane * 16);
 
+    if constexpr (KX == kQf) {  // full-attention layer: divide by the softmax sums
+        const float* dv = p.div + (size_t)(m0 + m) * kGf;
+#pragma unroll
+        for (int i = 0; i < RowStage<KX / 8>::N; ++i)
+            st.v[i] = o_input_chunk(st.v[i], dv, min((int)threadIdx.x + i * kBlock, KX / 8 - 1) * 8);
+    }
     row_finish(st, xs);
 
     float acc[R];
@@ -886,10 +960,10 @@ constexpr int kOEpochCounters = 16;
 static_assert(kPostGrid * kPostWgRows == kH && kOWaves * kORowsW == kPostWgRows, "O grid");
 static_assert(kPostGrid % kOEpochCounters == 0, "equal workgroups per epoch counter");
 
-template <ScaleKind SK>
+template <ScaleKind SK, int KX>
 __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, PostSlots* slots, uint32_t* tickets,
                                                           uint32_t* err) {
-    __shared__ uint16_t xs[kQs];
+    __shared__ uint16_t xs[KX];
     __shared__ uint32_t dl[kPostWgRows];
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kOWaves - 1;
@@ -906,20 +980,28 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
     }
     const int row0 = blockIdx.x * kPostWgRows + wave * kORowsW;
     const float scale = load_scale<SK>(p.os, row0 + min(lane, kORowsW - 1));
-    const uint4 xq = ld16(p.x + (size_t)m0 * kQs + threadIdx.x * 8);  // 512 chunks of 8
+    constexpr int XC = KX / 8 / kOBlock;  // 16-byte chunks of the row per thread
+    static_assert(XC * 8 * kOBlock == KX, "O row staging");
+    uint4 xq[XC];
+#pragma unroll
+    for (int i = 0; i < XC; ++i) xq[i] = ld16(p.x + (size_t)m0 * KX + (threadIdx.x + i * kOBlock) * 8);
     __syncthreads();
-    constexpr int KI = kQs / 1024;
+    constexpr int KI = KX / 1024;
     uint4 wq[kORowsW][KI];
 #pragma unroll
     for (int r = 0; r < kORowsW; ++r)
 #pragma unroll
-        for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * kQs + j * 1024 + lane * 16);
+        for (int j = 0; j < KI; ++j) wq[r][j] = ld_stream(p.ow + (size_t)(row0 + r) * KX + j * 1024 + lane * 16);
     // the epoch add behind the weights (loads retire in order: issued first, its return would
     // hold up every later wait of the wave)
     if (ctl && lane == 0)
         ep = counter_add(tickets + (kTicketOEpoch + blockIdx.x % kOEpochCounters) * kTicketStride) /
              (kPostGrid / kOEpochCounters);
-    *reinterpret_cast<uint4*>(xs + threadIdx.x * 8) = xq;
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int k = (threadIdx.x + i * kOBlock) * 8;
+        *reinterpret_cast<uint4*>(xs + k) = KX == kQf ? o_input_chunk(xq[i], p.div + (size_t)m0 * kGf, k) : xq[i];
+    }
     __syncthreads();
 
     float acc[kORowsW];
@@ -1501,8 +1583,22 @@ hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* c
         }
         const dim3 grid(kQkvRows / (4 * kQkvR), mm);
         hipError_t e = p.scale_kind == ScaleKind::F32
-            ? launch(qkv_decode_kernel<ScaleKind::F32>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err)
-            : launch(qkv_decode_kernel<ScaleKind::BF16>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err);
+            ? launch(qkv_decode_kernel<ScaleKind::F32, false>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err)
+            : launch(qkv_decode_kernel<ScaleKind::BF16, false>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_full_qkv(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    static_assert(kFqkvRows <= kL, "raw full-layer projections fit a pbuf row");
+    for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
+        const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        const dim3 grid(kFqkvRows / (4 * kQkvR), mm);
+        // raw projections in pbuf, rows kFqkvRows apart (pbuf holds kMaxChunkM x kL >= 16 x 8704)
+        hipError_t e = p.scale_kind == ScaleKind::F32
+            ? launch(qkv_decode_kernel<ScaleKind::F32, true>, grid, s, p, m0, ctx->pbuf, ctx->tickets, ctx->err)
+            : launch(qkv_decode_kernel<ScaleKind::BF16, true>, grid, s, p, m0, ctx->pbuf, ctx->tickets, ctx->err);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -1519,20 +1615,23 @@ static bool fits_resident(int8_t& known, K kernel, int block, int grid, const De
     return known == 1;
 }
 
-hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx) {
+template <int KX>
+static hipError_t o_decode_impl(const OParams& p, int M, hipStream_t s, DevCtx* ctx, int8_t* fused_known) {
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
         if (mm == 1) {
             const bool f32 = p.scale_kind == ScaleKind::F32;
             PostSlots* slots = reinterpret_cast<PostSlots*>(ctx->o_part);
-            if (f32 && fits_resident(ctx->o_fused[0], o_fused_kernel<ScaleKind::F32>, kOBlock, kPostGrid, ctx)) {
-                o_fused_kernel<ScaleKind::F32><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets, ctx->err);
+            if (f32 && fits_resident(fused_known[0], o_fused_kernel<ScaleKind::F32, KX>, kOBlock, kPostGrid, ctx)) {
+                o_fused_kernel<ScaleKind::F32, KX><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets,
+                                                                                            ctx->err);
                 const hipError_t e = hipGetLastError();
                 if (e != hipSuccess) return e;
                 continue;
             }
-            if (!f32 && fits_resident(ctx->o_fused[1], o_fused_kernel<ScaleKind::BF16>, kOBlock, kPostGrid, ctx)) {
-                o_fused_kernel<ScaleKind::BF16><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets, ctx->err);
+            if (!f32 && fits_resident(fused_known[1], o_fused_kernel<ScaleKind::BF16, KX>, kOBlock, kPostGrid, ctx)) {
+                o_fused_kernel<ScaleKind::BF16, KX><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets,
+                                                                                             ctx->err);
                 const hipError_t e = hipGetLastError();
                 if (e != hipSuccess) return e;
                 continue;
@@ -1540,11 +1639,19 @@ hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx) 
         }
         const dim3 grid(kH / (4 * kOR), mm);
         hipError_t e = p.scale_kind == ScaleKind::F32
-            ? launch(o_decode_kernel<ScaleKind::F32>, grid, s, p, m0, ctx->pbuf, ctx->tickets)
-            : launch(o_decode_kernel<ScaleKind::BF16>, grid, s, p, m0, ctx->pbuf, ctx->tickets);
+            ? launch(o_decode_kernel<ScaleKind::F32, KX>, grid, s, p, m0, ctx->pbuf, ctx->tickets)
+            : launch(o_decode_kernel<ScaleKind::BF16, KX>, grid, s, p, m0, ctx->pbuf, ctx->tickets);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    return o_decode_impl<kQs>(p, M, s, ctx, ctx->o_fused);
+}
+
+hipError_t launch_full_o(const OParams& p, int M, hipStream_t s, DevCtx* ctx) {
+    return o_decode_impl<kQf>(p, M, s, ctx, ctx->full_o_fused);
 }
 
 // Whether the single-launch FFN's grid fits on the device at once (checked once per device).

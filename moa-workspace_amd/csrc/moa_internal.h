@@ -40,6 +40,11 @@ constexpr int kTicketAttn = kTicketFfnEpoch + 16;
 constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;
 // sliding_attention partials: [kMaxDecodeM][kNs][32 chunks][kGs][max, sum, o[kDs]]
 constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (2 + kDs);
+// full-attention page partials: per token row and 64-slot chunk, 16 maxima, 16 sums, out [16][512]
+constexpr int kFaChunks = 8;
+constexpr int kFaDimBlocks = 4;
+constexpr int kFaRec = 2 * kGf + kGf * kDf;
+constexpr size_t kFattnPartFloats = (size_t)kMaxDecodeM * kFaChunks * kFaRec;
 
 // Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
 // never shared with another kernel).
@@ -67,11 +72,13 @@ struct DevCtx {
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
     float* attn_part = nullptr;   // sliding_attention split partials (kAttnPartFloats)
+    float* fattn_part = nullptr;  // full-attention page partials (kFattnPartFloats)
     void* base = nullptr;
     int cus = 0;                  // compute units of the device
     int8_t ffn_fused[6] = {-1, -1, -1, -1, -1, -1};  // per (format, scale kind): grid fits resident? (-1 unknown)
     int8_t o_fused[2] = {-1, -1};                    // per scale kind
     int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
+    int8_t full_o_fused[2] = {-1, -1};               // the same for full_attention_output
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
@@ -94,6 +101,7 @@ struct QkvParams {
 struct OParams {
     const uint16_t* x; const uint16_t* post_rms; const uint8_t* ow; const void* os; ScaleKind scale_kind;
     uint16_t* residual;
+    const float* div = nullptr;  // full-attention layers: running softmax sums [M][16] that divide x
 };
 
 struct FfnParams {
@@ -115,6 +123,16 @@ hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* c
 hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_decode(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s);
+
+// Full-attention layers: ops::full_project_qkv (QkvParams with vw / vs unused; k_cache / v_cache
+// are the position's page) and ops::full_attention_output (OParams with div set).
+hipError_t launch_full_qkv(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_full_o(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
+// ops::full_attention_first_page (first) / ops::full_attention_page for M token rows: q / out
+// [M][16][512], the page's K and V [512][512], mask [M][512], running max / sum [M][16].
+hipError_t launch_full_attention_page(const uint16_t* q, const uint16_t* k_page, const uint16_t* v_page,
+                                      const float* mask, float* running_max, float* running_sum, uint16_t* out,
+                                      int M, bool first, hipStream_t s, DevCtx* ctx);
 
 // MFMA path for one chunk of 1..kMaxChunkM token rows starting at row m0 of the call.
 hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);

@@ -60,6 +60,10 @@ SIGNATURES = {
     "moa_sliding_project_qkv_bf16_scales": [P] * 17 + [I32, P],
     "moa_sliding_attention": [P] * 5 + [I32, P],
     "moa_final_norm_and_logits": [P] * 4 + [I32, P],
+    "moa_full_project_qkv": [P] * 15 + [I32, P],
+    "moa_full_attention_first_page": [P] * 7 + [I32, P],
+    "moa_full_attention_page": [P] * 7 + [I32, P],
+    "moa_full_attention_output": [P] * 6 + [I32, P],
     "moa_sliding_attention_output": [P] * 5 + [I32, P],
     "moa_sliding_attention_output_bf16_scales": [P] * 5 + [I32, P],
     "moa_decoder_feedforward": [P] * 13 + [I32, P],

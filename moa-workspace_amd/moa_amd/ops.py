@@ -95,6 +95,59 @@ def sliding_attention(q, k, v, mask, out) -> None:
     _lib.call("moa_sliding_attention", *args, M, _stream(q))
 
 
+GF, DF, QF, PF, TF = 16, 512, 8192, 512, 512  # full-attention layers (FO/src/axes.rs)
+
+
+def full_project_qkv(x, q_weight, k_weight, q_weight_scale, k_weight_scale, input_rms_weight, q_rms_weight,
+                     k_rms_weight, kv_offset, rope_offset, cos, sin, k_cache, v_cache, q_out) -> None:
+    """ops::full_project_qkv (FO/src/ops.rs:78-116). k_cache / v_cache are the position's page
+    [512, 512]; V is the unweighted norm of the raw K projection. bf16 per-row weight scales."""
+    M = _rows(x, H, "x")
+    args = [
+        _ptr(x, "x", _BF16), _ptr(q_weight, "q_weight", _U8, QF * H), _ptr(k_weight, "k_weight", _U8, PF * H),
+        _ptr(q_weight_scale, "q_weight_scale", _BF16, QF), _ptr(k_weight_scale, "k_weight_scale", _BF16, PF),
+        _ptr(input_rms_weight, "input_rms_weight", _BF16, H), _ptr(q_rms_weight, "q_rms_weight", _BF16, DF),
+        _ptr(k_rms_weight, "k_rms_weight", _BF16, DF), _ptr(kv_offset, "kv_offset", _I32, 1),
+        _ptr(rope_offset, "rope_offset", _I32, 1), _ptr(cos, "cos", _BF16, E * DF), _ptr(sin, "sin", _BF16, E * DF),
+        _ptr(k_cache, "k_cache", _BF16, TF * DF), _ptr(v_cache, "v_cache", _BF16, TF * DF),
+        _ptr(q_out, "q_out", _BF16, M * QF),
+    ]
+    _lib.call("moa_full_project_qkv", *args, M, _stream(x))
+
+
+def _full_page(name, q, k, v, mask, running_max, running_sum, out):
+    M = _rows(q, QF, "q")
+    args = [
+        _ptr(q, "q", _BF16), _ptr(k, "k", _BF16, TF * DF), _ptr(v, "v", _BF16, TF * DF),
+        _ptr(mask, "mask", _F32, M * TF), _ptr(running_max, "running_max", _F32, M * GF),
+        _ptr(running_sum, "running_sum", _F32, M * GF), _ptr(out, "out", _BF16, M * QF),
+    ]
+    _lib.call(name, *args, M, _stream(q))
+
+
+def full_attention_first_page(q, k, v, mask, running_max, running_sum, out) -> None:
+    """ops::full_attention_first_page (FO/src/ops.rs:148-160): starts the running softmax state
+    (max, sum [M, 16] f32; out [M, 16, 512] bf16, un-normalised) from one 512-slot page."""
+    _full_page("moa_full_attention_first_page", q, k, v, mask, running_max, running_sum, out)
+
+
+def full_attention_page(q, k, v, mask, running_max, running_sum, out) -> None:
+    """ops::full_attention_page (FO/src/ops.rs:162-174): folds one more page into the state."""
+    _full_page("moa_full_attention_page", q, k, v, mask, running_max, running_sum, out)
+
+
+def full_attention_output(x, running_sum, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
+    """ops::full_attention_output (FO/src/ops.rs:176-199): x / running_sum, the O projection
+    (K = 8192, bf16 per-row scales), post-norm and residual add, in place."""
+    M = _rows(x, QF, "x")
+    args = [
+        _ptr(x, "x", _BF16), _ptr(running_sum, "running_sum", _F32, M * GF),
+        _ptr(post_attn_rms_weight, "post_attn_rms_weight", _BF16, H), _ptr(o_weight, "o_weight", _U8, H * QF),
+        _ptr(o_weight_scale, "o_weight_scale", _BF16, H), _ptr(residual, "residual", _BF16, M * H),
+    ]
+    _lib.call("moa_full_attention_output", *args, M, _stream(x))
+
+
 def final_norm_and_logits(input, rms_weight, lm_head_weight, out) -> None:
     """ops::final_norm_and_logits (FO/src/ops.rs:241-298): out = softcap30(bf16(RMSNorm(input) .
     lm_head_weight^T)). input [M, 3840] bf16, lm_head_weight [262144, 3840] bf16, out [M, 262144] bf16."""

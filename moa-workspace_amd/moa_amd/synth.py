@@ -242,6 +242,87 @@ def cfg_attention(seed: int = 0, M: int = 1, pos=1023, q_std: float = 1.0, tag: 
                 mask=attention_mask(M, pos))
 
 
+# ------------------------------------------------------------ full-attention layers
+
+GF, DF, QF, PF, TF = 16, 512, 8192, 512, 512
+
+
+def rope_tables_full(positions, theta: float = 1_000_000.0, rotated: int = 128):
+    """[E, 512] bf16 cos / sin of the full-attention layers as the runtime builds them
+    (FO/src/host/runtime.rs:298-322): f32 angles pos / theta^(2i / 512) for the first rotated / 2
+    entries of each half (25 % of the head), cos 1 and sin 0 beyond, the low half of sin negated.
+    Rows outside `positions` stay zero."""
+    half, rh = DF // 2, rotated // 2
+    i = np.arange(half)
+    den = np.power(np.float32(theta), (2 * i).astype(np.float32) / np.float32(DF)).astype(np.float32)
+    cos = np.zeros((E, DF), np.uint16)
+    sin = np.zeros((E, DF), np.uint16)
+    for p in positions:
+        freq = (np.float32(p) / den).astype(np.float32)
+        c = np.where(i < rh, np.cos(freq), np.float32(1.0)).astype(np.float32)
+        lo = np.where(i < rh, -np.sin(freq), np.float32(0.0)).astype(np.float32)
+        hi = np.where(i < rh, np.sin(freq), np.float32(0.0)).astype(np.float32)
+        cos[p] = prng.f32_to_bf16_bits(np.concatenate([c, c]))
+        sin[p] = prng.f32_to_bf16_bits(np.concatenate([lo, hi]))
+    return cos, sin
+
+
+def _bf16_scales(s):
+    return prng.f32_to_bf16_bits(np.asarray(s, np.float32))
+
+
+def cfg_full_qkv(seed: int = 0, M: int = 1, pos: int = 700, tag: str = "full") -> dict:
+    """full_project_qkv inputs for rows at positions pos .. pos + M - 1 (one page): FP8 Q [8192, 3840]
+    and K [512, 3840] with bf16 per-row scales, N(0, 1) activations, the page pre-filled N(0, 1)."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    qw, qs = fp8_weight(n("q"), QF, H)
+    kw, ks = fp8_weight(n("k"), PF, H)
+    cos, sin = rope_tables_full(range(pos, pos + M))
+    return dict(x=bf16_normal(n("x"), (M, H)), q_weight=qw, k_weight=kw, q_weight_scale=_bf16_scales(qs),
+                k_weight_scale=_bf16_scales(ks), input_rms_weight=rms_weight(n("in_rms"), H),
+                q_rms_weight=rms_weight(n("q_rms"), DF), k_rms_weight=rms_weight(n("k_rms"), DF), pos=pos,
+                rope_offset=pos * DF * 2, kv_offset=(pos % TF) * DF * 2, cos=cos, sin=sin,
+                k_cache=bf16_normal(n("k_page"), (TF, DF)), v_cache=bf16_normal(n("v_page"), (TF, DF)))
+
+
+def full_masks(P: int, pos) -> np.ndarray:
+    """[P, M, 512] mask rows of the runtime (FO/src/host/runtime.rs:159-165, 496-503) for rows at
+    positions `pos`: 1.0 over pages before the position's page, its diagonal row on that page
+    (slots <= pos % 512), 0.0 on later pages."""
+    pos = np.atleast_1d(np.asarray(pos))
+    out = np.zeros((P, pos.size, TF), np.float32)
+    for m, p in enumerate(pos):
+        page, row = int(p) // TF, int(p) % TF
+        for pg in range(P):
+            if pg < page:
+                out[pg, m] = 1.0
+            elif pg == page:
+                out[pg, m, : row + 1] = 1.0
+    return out
+
+
+def cfg_full_attention(seed: int = 0, M: int = 1, P: int = 2, pos=None, q_std: float = 1.0,
+                       tag: str = "fattn") -> dict:
+    """Full-attention pages: q [M, 16, 512] ~ N(0, q_std) (1.0: unit-RMS heads, as after the q
+    norm), P pages of K and V [512, 512] ~ N(0, 1), and the runtime's masks for positions `pos`
+    (default: the last slot of page P - 1)."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    if pos is None:
+        pos = [P * TF - 1] * M
+    return dict(q=bf16_normal(n("q"), (M, GF, DF), q_std), k_pages=bf16_normal(n("k"), (P, TF, DF)),
+                v_pages=bf16_normal(n("v"), (P, TF, DF)), masks=full_masks(P, pos))
+
+
+def cfg_full_o(seed: int = 0, M: int = 1, tag: str = "fo") -> dict:
+    """full_attention_output inputs: x [M, 16, 512] (un-normalised sums, ~ N(0, 4)), running sums
+    [M, 16] in [1, 50), FP8 W_o [3840, 8192] with bf16 per-row scales, post-norm weight, residual."""
+    n = lambda t: f"{tag}.seed{seed}.{t}"
+    ow, os_ = fp8_weight(n("o"), H, QF)
+    rs = (1.0 + 49.0 * _gen(n("sum")).random((M, GF))).astype(np.float32)
+    return dict(x=bf16_normal(n("x"), (M, GF, DF), 4.0), running_sum=rs, post_attn_rms_weight=rms_weight(n("post"), H),
+                o_weight=ow, o_weight_scale=_bf16_scales(os_), residual=bf16_normal(n("residual"), (M, H)))
+
+
 def lm_head_bits(r):
     """bf16 lm_head values from random integers r in [0, 65536) (numpy or torch int32): the sign and
     mantissa bits of r, exponent 2^-5 .. 2^-2 from two more bits, so |w| lies in [1/32, 1/2) with an

@@ -277,21 +277,25 @@ void orc_scaled_projection_fp8(const uint16_t* x, int M, int K, const uint8_t* w
 
 /* --------------------------------------------------------------------- QKV */
 
-static void rope_head(const uint16_t* xin, const uint16_t* cos_row, const uint16_t* sin_dev,
-                      uint16_t* out) {
+static void rope_head_n(const uint16_t* xin, const uint16_t* cos_row, const uint16_t* sin_dev,
+                        uint16_t* out, int n) {
     /* generate_references.py:213-220 with gemma4.py:120-122: y = x*cos + rotate_half(x)*sin,
-     * every op rounded to bf16. The table holds sin with the low half negated
-     * (generate_references.py:200-210); undo that exactly to recover the reference sin. */
-    for (int i = 0; i < ORC_DS; ++i) {
+     * every op rounded to bf16, over a head of n elements. The table holds sin with the low half
+     * negated (generate_references.py:200-210; runtime.rs:298-322); undo that exactly to recover
+     * the reference sin. */
+    for (int i = 0; i < n; ++i) {
         float s = orc_bf16_to_f32(sin_dev[i]);
-        if (i < ORC_DS / 2) s = -s;
+        if (i < n / 2) s = -s;
         float xi = orc_bf16_to_f32(xin[i]);
-        float rot = i < ORC_DS / 2 ? -orc_bf16_to_f32(xin[i + ORC_DS / 2])
-                                   : orc_bf16_to_f32(xin[i - ORC_DS / 2]);
+        float rot = i < n / 2 ? -orc_bf16_to_f32(xin[i + n / 2]) : orc_bf16_to_f32(xin[i - n / 2]);
         float a = orc_bf16_to_f32(orc_bf16_rne(xi * orc_bf16_to_f32(cos_row[i])));
         float b = orc_bf16_to_f32(orc_bf16_rne(rot * orc_bf16_to_f32(orc_bf16_rne(s))));
         out[i] = orc_bf16_rne(a + b);
     }
+}
+
+static void rope_head(const uint16_t* xin, const uint16_t* cos_row, const uint16_t* sin_dev, uint16_t* out) {
+    rope_head_n(xin, cos_row, sin_dev, out, ORC_DS);
 }
 
 void orc_sliding_project_qkv(const uint16_t* x, const uint8_t* q_w, const uint8_t* k_w,
@@ -329,6 +333,92 @@ void orc_sliding_project_qkv(const uint16_t* x, const uint8_t* q_w, const uint8_
     free(q_raw);
     free(k_raw);
     free(v_raw);
+}
+
+/* ------------------------------------------------------ full-attention layer */
+
+void orc_full_project_qkv(const uint16_t* x, const uint8_t* q_w, const uint8_t* k_w, const float* q_s,
+                          const float* k_s, const uint16_t* in_rms, const uint16_t* q_rms, const uint16_t* k_rms,
+                          int32_t kv_offset, int32_t rope_offset, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                          uint16_t* k_page, uint16_t* v_page, uint16_t* q_out, int M) {
+    uint16_t h[ORC_H];
+    uint16_t* q_raw = (uint16_t*)malloc(2 * ORC_QF);
+    uint16_t k_raw[ORC_DF], tmp[ORC_DF];
+    const int slot0 = kv_offset / (ORC_DF * 2);
+    const int row0 = rope_offset / (ORC_DF * 2);
+    for (int m = 0; m < M; ++m) {
+        orc_rmsnorm_row(x + (size_t)m * ORC_H, in_rms, ORC_H, h);
+        orc_scaled_projection_fp8(h, 1, ORC_H, q_w, q_s, ORC_QF, q_raw);
+        orc_scaled_projection_fp8(h, 1, ORC_H, k_w, k_s, ORC_DF, k_raw);
+        const uint16_t* cos_row = cos_tab + (size_t)(row0 + m) * ORC_DF;
+        const uint16_t* sin_row = sin_tab + (size_t)(row0 + m) * ORC_DF;
+        for (int hd = 0; hd < ORC_GF; ++hd) {
+            orc_rmsnorm_row(q_raw + hd * ORC_DF, q_rms, ORC_DF, tmp);
+            rope_head_n(tmp, cos_row, sin_row, q_out + ((size_t)m * ORC_QF + hd * ORC_DF), ORC_DF);
+        }
+        const size_t at = (size_t)(slot0 + m) * ORC_DF;
+        orc_rmsnorm_row(k_raw, k_rms, ORC_DF, tmp);
+        rope_head_n(tmp, cos_row, sin_row, k_page + at, ORC_DF);
+        orc_rmsnorm_row(k_raw, NULL, ORC_DF, v_page + at); /* V: the unweighted norm of raw K */
+    }
+    free(q_raw);
+}
+
+void orc_full_attention_pages(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                              const float* masks, int P, float* running_max, float* running_sum, uint16_t* out,
+                              int M) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int m = 0; m < M; ++m)
+        for (int hd = 0; hd < ORC_GF; ++hd) {
+            const uint16_t* qr = q + ((size_t)m * ORC_GF + hd) * ORC_DF;
+            double* s = (double*)malloc(sizeof(double) * (size_t)P * ORC_TF);
+            double mx = -INFINITY;
+            for (int pg = 0; pg < P; ++pg)
+                for (int t = 0; t < ORC_TF; ++t) {
+                    const size_t at = (size_t)pg * ORC_TF + t;
+                    if (masks[((size_t)pg * M + m) * ORC_TF + t] == 0.0f) continue;
+                    const uint16_t* kr = k_pages + at * ORC_DF;
+                    double a = 0.0;
+                    for (int d = 0; d < ORC_DF; ++d) a += (double)orc_bf16_to_f32(qr[d]) * orc_bf16_to_f32(kr[d]);
+                    s[at] = a;
+                    if (a > mx) mx = a;
+                }
+            double l = 0.0, o[ORC_DF];
+            for (int d = 0; d < ORC_DF; ++d) o[d] = 0.0;
+            if (mx != -INFINITY) {
+                for (int pg = 0; pg < P; ++pg)
+                    for (int t = 0; t < ORC_TF; ++t) {
+                        const size_t at = (size_t)pg * ORC_TF + t;
+                        if (masks[((size_t)pg * M + m) * ORC_TF + t] == 0.0f) continue;
+                        const double e = exp(s[at] - mx);
+                        l += e;
+                        const uint16_t* vr = v_pages + at * ORC_DF;
+                        for (int d = 0; d < ORC_DF; ++d) o[d] += e * orc_bf16_to_f32(vr[d]);
+                    }
+            }
+            running_max[(size_t)m * ORC_GF + hd] = (float)mx;
+            running_sum[(size_t)m * ORC_GF + hd] = (float)l;
+            uint16_t* orow = out + ((size_t)m * ORC_GF + hd) * ORC_DF;
+            for (int d = 0; d < ORC_DF; ++d) orow[d] = orc_bf16_rne((float)o[d]);
+            free(s);
+        }
+}
+
+void orc_full_attention_output(const uint16_t* x, const float* running_sum, const uint16_t* post_rms,
+                               const uint8_t* o_w, const float* o_s, uint16_t* residual, int M) {
+    uint16_t* xd = (uint16_t*)malloc(2 * ORC_QF);
+    uint16_t p[ORC_H], n[ORC_H];
+    for (int m = 0; m < M; ++m) {
+        for (int i = 0; i < ORC_QF; ++i) {
+            const float sm = running_sum[(size_t)m * ORC_GF + i / ORC_DF];
+            xd[i] = orc_bf16_rne(sm > 0.0f ? orc_bf16_to_f32(x[(size_t)m * ORC_QF + i]) / sm : 0.0f);
+        }
+        orc_scaled_projection_fp8(xd, 1, ORC_QF, o_w, o_s, ORC_H, p);
+        orc_rmsnorm_row(p, post_rms, ORC_H, n);
+        uint16_t* r = residual + (size_t)m * ORC_H;
+        for (int i = 0; i < ORC_H; ++i) r[i] = orc_bf16_rne(orc_bf16_to_f32(r[i]) + orc_bf16_to_f32(n[i]));
+    }
+    free(xd);
 }
 
 /* ---------------------------------------------------------------------- O */

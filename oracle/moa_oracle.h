@@ -31,7 +31,8 @@ extern "C" {
 /* ---- shapes (FO/src/axes.rs:3-29, FO/src/lib.rs:25) ---- */
 enum {
     ORC_H = 3840, ORC_L = 15360, ORC_NS = 8, ORC_GS = 2, ORC_DS = 256,
-    ORC_QS = 4096, ORC_PS = 2048, ORC_TS = 1024, ORC_E = 32768
+    ORC_QS = 4096, ORC_PS = 2048, ORC_TS = 1024, ORC_E = 32768,
+    ORC_GF = 16, ORC_DF = 512, ORC_QF = 8192, ORC_TF = 512 /* full-attention layers */
 };
 #define ORC_EPS 1e-6f
 
@@ -93,6 +94,29 @@ void orc_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t*
  * x [M,4096]; o_w [3840,4096]; residual [M,3840] updated in place. */
 void orc_sliding_attention_output(const uint16_t* x, const uint16_t* post_rms, const uint8_t* o_w,
                                   const float* o_s, uint16_t* residual, int M);
+
+/* ops::full_project_qkv (FO/src/ops.rs:78-116; gemma4.py:152-166 with attention_k_eq_v):
+ * x [M,3840]; q_w [8192,3840], k_w [512,3840] E4M3 with f32 row scales; q_rms, k_rms [512];
+ * cos/sin [E][512] (sin's low half negated). Row m: q_out [M][16][512]; slot kv_offset/1024 + m
+ * of the page gets K = RoPE(RMSNorm(k_raw, k_rms)) in k_page and V = RMSNorm(k_raw) in v_page
+ * ([512][512] each); RoPE row rope_offset/1024 + m. */
+void orc_full_project_qkv(const uint16_t* x, const uint8_t* q_w, const uint8_t* k_w, const float* q_s,
+                          const float* k_s, const uint16_t* in_rms, const uint16_t* q_rms, const uint16_t* k_rms,
+                          int32_t kv_offset, int32_t rope_offset, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                          uint16_t* k_page, uint16_t* v_page, uint16_t* q_out, int M);
+/* The running state of full_attention_first_page + full_attention_page over P pages
+ * (FO/src/ops.rs:148-174) computed at once in f64: the softmax of the CPU reference (gemma4.py:
+ * 180-184, scale 1.0) over the valid slots (mask != 0). q [M][16][512]; k_pages, v_pages
+ * [P][512][512]; masks [P][M][512]. running_max / running_sum [M][16]: the largest valid score
+ * and sum of exp(s - max); out [M][16][512] = bf16(sum of exp(s - max) v). No valid slot: -inf,
+ * 0 and zeros. */
+void orc_full_attention_pages(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                              const float* masks, int P, float* running_max, float* running_sum, uint16_t* out,
+                              int M);
+/* ops::full_attention_output (FO/src/ops.rs:176-199): x' = bf16(x / running_sum[head]) (0 for a
+ * zero sum), then as sliding_attention_output with K = 8192: residual += RMSNorm(bf16(x'.W_o^T * s)). */
+void orc_full_attention_output(const uint16_t* x, const float* running_sum, const uint16_t* post_rms,
+                               const uint8_t* o_w, const float* o_s, uint16_t* residual, int M);
 
 /* Gemma's final-logit softcap of a bf16 logit l (FO/src/ops.rs:256-293; gemma4.py:260-261):
  * tanh(l / 30) * 30 in f64, rounded once to bf16. */

@@ -73,6 +73,9 @@ def _declare(l: C.CDLL) -> None:
     l.orc_sliding_project_qkv.argtypes = [P] * 10 + [C.c_int32, C.c_int32] + [P] * 5 + [C.c_int]
     l.orc_sliding_attention_output.argtypes = [P, P, P, P, P, C.c_int]
     l.orc_sliding_attention.argtypes = [P, P, P, P, P, C.c_int]
+    l.orc_full_project_qkv.argtypes = [P] * 8 + [C.c_int32, C.c_int32] + [P] * 5 + [C.c_int]
+    l.orc_full_attention_pages.argtypes = [P, P, P, P, C.c_int, P, P, P, C.c_int]
+    l.orc_full_attention_output.argtypes = [P] * 6 + [C.c_int]
     l.orc_softcap30.argtypes = [C.c_uint16]
     l.orc_softcap30.restype = C.c_uint16
     l.orc_final_norm_and_logits.argtypes = [P, P, P, C.c_int, P, C.c_int]
@@ -243,6 +246,47 @@ def sliding_attention(q, k, v, mask):
     out = np.zeros((M, QS), np.uint16)
     lib().orc_sliding_attention(_p(q), _p(_u16(k)), _p(_u16(v)), _p(mask), _p(out), M)
     return out.reshape(M, NS, GS, DS)
+
+
+GF, DF, QF, TF = 16, 512, 8192, 512
+
+
+def full_project_qkv(x, q_w, k_w, q_s, k_s, in_rms, q_rms, k_rms, kv_offset, rope_offset, cos, sin,
+                     k_page, v_page, q_out):
+    """ops::full_project_qkv (FO/src/ops.rs:78-116). Updates k_page / v_page / q_out in place."""
+    x = _u16(x).reshape(-1, H)
+    f = lambda s: np.ascontiguousarray(s, dtype=np.float32)
+    for a in (k_page, v_page, q_out):
+        assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
+    lib().orc_full_project_qkv(_p(x), _p(np.ascontiguousarray(q_w)), _p(np.ascontiguousarray(k_w)), _p(f(q_s)),
+                               _p(f(k_s)), _p(_u16(in_rms)), _p(_u16(q_rms)), _p(_u16(k_rms)), int(kv_offset),
+                               int(rope_offset), _p(_u16(cos)), _p(_u16(sin)), _p(k_page), _p(v_page), _p(q_out),
+                               x.shape[0])
+
+
+def full_attention_pages(q, k_pages, v_pages, masks):
+    """The state after full_attention_first_page + full_attention_page over the given pages
+    (FO/src/ops.rs:148-174). k_pages / v_pages [P, 512, 512] bf16; masks [P, M, 512] f32.
+    Returns (running_max [M, 16] f32, running_sum [M, 16] f32, out [M, 16, 512] bf16 bits)."""
+    q = _u16(q).reshape(-1, QF)
+    M = q.shape[0]
+    k_pages = _u16(k_pages).reshape(-1, TF, DF)
+    P = k_pages.shape[0]
+    masks = np.ascontiguousarray(masks, dtype=np.float32).reshape(P, M, TF)
+    mx = np.zeros((M, GF), np.float32)
+    sm = np.zeros((M, GF), np.float32)
+    out = np.zeros((M, GF, DF), np.uint16)
+    lib().orc_full_attention_pages(_p(q), _p(k_pages), _p(_u16(v_pages)), _p(masks), P, _p(mx), _p(sm), _p(out), M)
+    return mx, sm, out
+
+
+def full_attention_output(x, running_sum, post_rms, o_w, o_s, residual):
+    """ops::full_attention_output (FO/src/ops.rs:176-199). Updates residual in place."""
+    x = _u16(x).reshape(-1, QF)
+    assert residual.dtype == np.uint16 and residual.flags["C_CONTIGUOUS"]
+    lib().orc_full_attention_output(_p(x), _p(np.ascontiguousarray(running_sum, dtype=np.float32)),
+                                    _p(_u16(post_rms)), _p(np.ascontiguousarray(o_w)),
+                                    _p(np.ascontiguousarray(o_s, dtype=np.float32)), _p(residual), x.shape[0])
 
 
 def softcap30(l: int) -> int:
