@@ -47,11 +47,18 @@ METRIC = "FFN/QKV/O decode µs/token at M=1 and % of HBM roofline (FP8 weights)"
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec
 MALL_BYTES = 256 << 20
 # Algorithmic bytes per call (weights + scales + operator-boundary vectors).
+FATTN_PAGES = 8  # full-attention decode at position 4095: pages 0..7
 BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          # sliding_attention, all 1024 slots valid: K and V caches + q + out + mask row
          "attn": 2 * 1024 * 8 * 256 * 2 + 2 * 4096 * 2 + 1024 * 4,
          # final_norm_and_logits: the bf16 lm_head (262144 x 3840) + input + norm weight + logits
-         "logits": 262144 * 3840 * 2 + 2 * 3840 * 2 + 262144 * 2}
+         "logits": 262144 * 3840 * 2 + 2 * 3840 * 2 + 262144 * 2,
+         # full-attention layers: QKV (Q 8192 + K 512 FP8 rows, bf16 scales; x, norms, cos/sin rows,
+         # q_out, one K and one V slot), O with K = 8192 (weights, scales, x, sums, norm weight,
+         # residual read + write), and the pages of a token at position 4095 (8 pages of K and V)
+         "fqkv": 8704 * 3840 + 8704 * 2 + 3840 * 2 * 2 + 512 * 2 * 2 + 2 * 512 * 2 + 8192 * 2 + 2 * 512 * 2,
+         "fo": 3840 * 8192 + 3840 * 2 + 8192 * 2 + 16 * 4 + 3840 * 2 + 2 * 3840 * 2,
+         "fattn": FATTN_PAGES * 2 * 512 * 512 * 2 + FATTN_PAGES * (8192 * 2 + 512 * 4 + 8192 * 2 * 2 + 16 * 4 * 4)}
 GRAPH_CALLS = 40  # calls per captured graph
 # Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
 FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
@@ -70,7 +77,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
-    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "chunk"), default=None,
+    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fo", "chunk"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     args = ap.parse_args()
@@ -117,6 +124,24 @@ def main() -> int:
     lg = synth.cfg_logits(0)
     lg_in, lg_rms, lg_w = dev(lg["input"]), dev(lg["rms_weight"]), synth.lm_head_device(0)
     lg_out = torch.zeros(synth.W, dtype=torch.int16, device="cuda")
+    # full-attention layer operators: weights rotated like the others, the pages of position 4095
+    fq = synth.cfg_full_qkv(0, pos=4095)
+    fo = synth.cfg_full_o(0)
+    fa = synth.cfg_full_attention(0, M=1, P=FATTN_PAGES)
+    nfq, nfo, nfa = copies(BYTES["fqkv"]), copies(BYTES["fo"]), copies(BYTES["fattn"])
+    FQW = replicate(fq, ("q_weight", "k_weight", "q_weight_scale", "k_weight_scale"), nfq)
+    FOW = replicate(fo, ("o_weight", "o_weight_scale"), nfo)
+    FAW = replicate(fa, ("k_pages", "v_pages"), nfa)
+    fq_d = {k: dev(fq[k]) for k in ("x", "input_rms_weight", "q_rms_weight", "k_rms_weight", "cos", "sin",
+                                    "k_cache", "v_cache")}
+    fq_out = torch.zeros(8192, dtype=torch.int16, device="cuda")
+    fq_kv = torch.tensor([fq["kv_offset"]], dtype=torch.int32, device="cuda")
+    fq_ro = torch.tensor([fq["rope_offset"]], dtype=torch.int32, device="cuda")
+    fo_d = {k: dev(fo[k]) for k in ("x", "running_sum", "post_attn_rms_weight", "residual")}
+    fa_q, fa_masks = dev(fa["q"]), dev(fa["masks"])
+    fa_max = torch.zeros(16, dtype=torch.float32, device="cuda")
+    fa_sum = torch.zeros(16, dtype=torch.float32, device="cuda")
+    fa_out = torch.zeros(8192, dtype=torch.int16, device="cuda")
     f_res, f_pre, f_post, f_ls = (dev(ffn[k]) for k in ("residual", "pre_ff_rms_weight", "post_ff_rms_weight",
                                                           "layer_scalar"))
     o_x, o_post, o_res = dev(o["x"]), dev(o["post_attn_rms_weight"]), dev(o["residual"])
@@ -181,6 +206,23 @@ def main() -> int:
         w = AW[i % na]
         ops.sliding_attention(a_q, w["k_cache"], w["v_cache"], a_mask, a_out)
 
+    def run_fqkv(i):
+        w = FQW[i % nfq]
+        ops.full_project_qkv(fq_d["x"], w["q_weight"], w["k_weight"], w["q_weight_scale"], w["k_weight_scale"],
+                             fq_d["input_rms_weight"], fq_d["q_rms_weight"], fq_d["k_rms_weight"], fq_kv, fq_ro,
+                             fq_d["cos"], fq_d["sin"], fq_d["k_cache"], fq_d["v_cache"], fq_out)
+
+    def run_fo(i):
+        w = FOW[i % nfo]
+        ops.full_attention_output(fo_d["x"], fo_d["running_sum"], fo_d["post_attn_rms_weight"], w["o_weight"],
+                                  w["o_weight_scale"], fo_d["residual"])
+
+    def run_fattn(i):
+        w = FAW[i % nfa]
+        for pg in range(FATTN_PAGES):
+            fn = ops.full_attention_first_page if pg == 0 else ops.full_attention_page
+            fn(fa_q, w["k_pages"][pg], w["v_pages"][pg], fa_masks[pg], fa_max, fa_sum, fa_out)
+
     def run_logits(i):
         ops.final_norm_and_logits(lg_in, lg_rms, lg_w, lg_out)
 
@@ -226,6 +268,7 @@ def main() -> int:
 
     if args.profile:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
+              "fqkv": run_fqkv, "fattn": run_fattn, "fo": run_fo,
               "chunk": run_layer}[args.profile]
         for i in range(args.steps):
             fn(i)
@@ -239,7 +282,8 @@ def main() -> int:
         return 0
 
     per_op = {}
-    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn), ("logits", run_logits)):
+    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn), ("logits", run_logits),
+                     ("fqkv", run_fqkv), ("fattn", run_fattn), ("fo", run_fo)):
         ms, _ = graph_timed(fn, args.steps, args.warmup)
         ms_host = timed(fn, min(args.steps, 50), 5)
         gbps = BYTES[name] / (ms * 1e-3) / 1e9
