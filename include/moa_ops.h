@@ -173,6 +173,14 @@ int moa_full_attention_first_page(const uint16_t* q, const uint16_t* k, const ui
 int moa_full_attention_page(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask,
                             float* running_max, float* running_sum, uint16_t* out, int M, void* stream);
 
+/* The state that full_attention_first_page followed by full_attention_page over pages 1 .. P-1
+ * leaves, in two launches whatever P is (no counterpart in the reference, whose runtime launches
+ * one operator per page, FO/src/host/runtime.rs:496-517). k_pages, v_pages bf16 [P,512,512]
+ * contiguous (page p at p * 512 * 512); masks f32 [P,M,512]; 1 <= P <= 64. Same outputs and
+ * meaning as the per-page calls. */
+int moa_full_attention(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages, const float* masks, int P,
+                       float* running_max, float* running_sum, uint16_t* out, int M, void* stream);
+
 /* ops::full_attention_output -- FO/src/ops.rs:176-199. x bf16 [M,16,512] (the pages' out),
  * running_sum f32 [M,16]; residual bf16 [M,3840] updated in place:
  * r = bf16(r + RMSNorm(bf16(bf16(x / sum) . W_o) * s)) with o_weight E4M3 [3840,8192] and bf16

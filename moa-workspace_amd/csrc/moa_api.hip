@@ -373,6 +373,21 @@ int moa_full_attention_page(const uint16_t* q, const uint16_t* k, const uint16_t
     return full_page(q, k, v, mask, running_max, running_sum, out, M, false, stream);
 }
 
+int moa_full_attention(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages, const float* masks, int P,
+                       float* running_max, float* running_sum, uint16_t* out, int M, void* stream) {
+    Check c;
+    c.ptr(q, "q").ptr(k_pages, "k_pages").ptr(v_pages, "v_pages").ptr(masks, "masks", 4);
+    c.ptr(running_max, "running_max", 4).ptr(running_sum, "running_sum", 4).ptr(out, "out").rows(M);
+    if (c.code) return c.code;
+    if (P < 1 || P > kCf) return fail(MOA_ERROR_INVALID_VALUE, "P must be in [1, 64], got " + std::to_string(P));
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return finish(launch_full_attention(q, k_pages, v_pages, masks, P, running_max, running_sum, out, M,
+                                        static_cast<hipStream_t>(stream), ctx),
+                  "full_attention launch");
+}
+
 int moa_full_attention_output(const uint16_t* x, const float* running_sum, const uint16_t* post_attn_rms_weight,
                               const uint8_t* o_weight, const uint16_t* o_weight_scale, uint16_t* residual, int M,
                               void* stream) {

@@ -24,6 +24,11 @@
 //     every weight). It writes the chunk's per-head max, sum and partial out (f32).
 //  2. fattn_combine_kernel, grid (16 heads, M): merges the 8 chunks with the old state and writes
 //     the new one. One workgroup owns a head's state, so no other reads it while it is replaced.
+//
+// moa_full_attention computes the same state over pages 0 .. P - 1 in two launches instead of 2 P:
+// the partial pass runs over every page at once (a workgroup takes a span of up to 8 chunks with an
+// online softmax, so a row has at most 64 records), and fattn_merge_kernel merges the records with
+// a grid of (16 heads, 4 dim blocks): no old state is read, so the split is free of races.
 #include <hip/hip_runtime.h>
 
 #include "moa_device.h"
@@ -44,103 +49,140 @@ static_assert(kFaChunks * kFaChunk == kTf && kFaRec == 2 * kGf + kGf * kDf, "ful
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
+// Workgroup (x, b, m) of the partial pass: chunks u = x * cpw .. min(x * cpw + cpw, nchunks) - 1 of
+// the row's slots (chunk u = slots 64 (u % 8) .. + 63 of page u / 8; pages lie kTf * kDf apart),
+// dims 128 b .. 128 b + 127 of V. Across its chunks it keeps an online softmax per head: the
+// running max, the sum of exp and out for its dims, rescaled whenever the max grows. Its record
+// of part (record x of row m, kFaRec floats): max[16], sum[16], out[16][512] (its 128 dims).
+// The next chunk's K rows and V slice are requested while the current chunk's weights and
+// products are computed.
 __global__ __launch_bounds__(kFaBlock) void fattn_partial_kernel(const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ kc,
                                                                  const uint16_t* __restrict__ vc,
-                                                                 const float* __restrict__ mask, float* part) {
+                                                                 const float* __restrict__ mask, int mask_page_stride,
+                                                                 int nchunks, int cpw, float* part) {
     __shared__ __attribute__((aligned(16))) uint16_t vs[kFaChunk * kFaVStride];
     __shared__ __attribute__((aligned(16))) uint16_t ps[2][kGf * kFaPStride];  // exp weights: bf16 high, low parts
     __shared__ float red_m[4][kGf], red_l[4][kGf];
-    const int c = blockIdx.x, b = blockIdx.y, m = blockIdx.z;
+    const int b = blockIdx.y, m = blockIdx.z;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int slot0 = c * kFaChunk;
+    const int u0 = blockIdx.x * cpw, u1 = min(u0 + cpw, nchunks);
 
-    // Wave w scores slots 16 w .. 16 w + 15 of the chunk. Lane l feeds K row (l % 16) and query
-    // head (l % 16), k 32 j + 8 (l / 16) .. + 7 of step j.
-    const int sl = slot0 + 16 * wave + l16;
-    uint4 kb[kDf / 32], qa[kDf / 32];
+    // Lane l of wave w feeds slot 16 w + (l % 16) of the chunk as a K row and query head l % 16,
+    // k 32 j + 8 (l / 16) .. + 7 of step j; the V slice (64 rows x 128 dims = 1024 units of 16
+    // bytes) is spread as units t + 256 i.
+    uint4 qa[kDf / 32], kb[kDf / 32], vv[4];
+    float mk = 0.0f;
+    auto issue = [&](int u) {
+        const int page = u / kFaChunks, sl = (u % kFaChunks) * kFaChunk + 16 * wave + l16;
+        const uint16_t* kp = kc + ((size_t)page * kTf + sl) * kDf + 8 * g;
 #pragma unroll
-    for (int j = 0; j < kDf / 32; ++j) kb[j] = ld16(kc + (size_t)sl * kDf + 32 * j + 8 * g);
+        for (int j = 0; j < kDf / 32; ++j) kb[j] = ld16(kp + 32 * j);
+        const uint16_t* vp = vc + ((size_t)page * kTf + (u % kFaChunks) * kFaChunk) * kDf + b * kFaDims;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int un = t + kFaBlock * i, row = un >> 4, cu = un & 15;
+            vv[i] = ld16(vp + (size_t)row * kDf + cu * 8);
+        }
+        mk = mask[(size_t)page * mask_page_stride + (size_t)m * kTf + sl];
+    };
+    issue(u0);
 #pragma unroll
     for (int j = 0; j < kDf / 32; ++j) qa[j] = ld16(q + (size_t)m * kQf + l16 * kDf + 32 * j + 8 * g);
-    // the chunk's V slice: 64 rows x 128 dims = 1024 units of 16 bytes, thread t takes t + 256 i
-    uint4 vv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int u = t + kFaBlock * i, row = u >> 4, cu = u & 15;
-        vv[i] = ld16(vc + (size_t)(slot0 + row) * kDf + b * kFaDims + cu * 8);
-    }
-    const bool valid = mask[(size_t)m * kTf + sl] != 0.0f;
 
-    f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < kDf / 32; ++j)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[j]), as_bf16x8(kb[j]), acc, 0, 0, 0);
-    // acc[r]: score of head 4 (l / 16) + r at slot sl
-    float sc[4], mx[4];
+    float m_run[4], l_run[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        sc[r] = valid ? acc[r] : -INFINITY;
-        mx[r] = sc[r];
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], o));
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.0f;
     }
-    if (l16 == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red_m[wave][4 * g + r] = mx[r];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int u = t + kFaBlock * i, row = u >> 4, cu = u & 15;
-        uint2* dst = reinterpret_cast<uint2*>(vs + row * kFaVStride + cu * 8);
-        dst[0] = make_uint2(vv[i].x, vv[i].y);
-        dst[1] = make_uint2(vv[i].z, vv[i].w);
-    }
-    __syncthreads();
-    float ls[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int h = 4 * g + r;
-        const float mh = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
-        const float pv = sc[r] == -INFINITY ? 0.0f : __expf(sc[r] - mh);
-        const uint32_t hi = f2bf(pv);
-        ps[0][h * kFaPStride + 16 * wave + l16] = (uint16_t)hi;
-        ps[1][h * kFaPStride + 16 * wave + l16] = (uint16_t)f2bf(pv - bf2f(hi));
-        ls[r] = pv;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) ls[r] += __shfl_xor(ls[r], o);
-    }
-    if (l16 == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red_l[wave][4 * g + r] = ls[r];
-    }
-    __syncthreads();
-
-    // out[h][d] = sum_s p[h][s] v[s][d]: wave w takes dims 32 w .. 32 w + 31 of the block (two
-    // 16-column tiles), the 64 slots as two k steps of 32. A: weights of head l % 16, slots
-    // 32 kk + 8 (l / 16) .. + 7; B: V at those slots, dim l % 16 of the tile.
     f32x4v o[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    for (int u = u0; u < u1; ++u) {
+        __syncthreads();  // the previous chunk's LDS reads are done
+        const bool valid = mk != 0.0f;
+        f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        const uint4 a = *reinterpret_cast<const uint4*>(ps[0] + l16 * kFaPStride + 32 * kk + 8 * g);
-        const uint4 al = *reinterpret_cast<const uint4*>(ps[1] + l16 * kFaPStride + 32 * kk + 8 * g);
+        for (int j = 0; j < kDf / 32; ++j)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[j]), as_bf16x8(kb[j]), acc, 0, 0, 0);
+        // acc[r]: score of head 4 (l / 16) + r at the lane's slot
+        float sc[4], mx[4];
 #pragma unroll
-        for (int dd = 0; dd < 2; ++dd) {
-            const int col = 32 * wave + 16 * dd + l16;
-            const uint16_t* vp = vs + (32 * kk + 8 * g) * kFaVStride + col;
-            uint32_t w[4];
+        for (int r = 0; r < 4; ++r) {
+            sc[r] = valid ? acc[r] : -INFINITY;
+            mx[r] = sc[r];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = (uint32_t)vp[(2 * i) * kFaVStride] | ((uint32_t)vp[(2 * i + 1) * kFaVStride] << 16);
-            const bf16x8 bv = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
-            o[dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), bv, o[dd], 0, 0, 0);
-            o[dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al), bv, o[dd], 0, 0, 0);
+            for (int sh = 1; sh < 16; sh <<= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], sh));
+        }
+        if (l16 == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red_m[wave][4 * g + r] = mx[r];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int un = t + kFaBlock * i, row = un >> 4, cu = un & 15;
+            uint2* dst = reinterpret_cast<uint2*>(vs + row * kFaVStride + cu * 8);
+            dst[0] = make_uint2(vv[i].x, vv[i].y);
+            dst[1] = make_uint2(vv[i].z, vv[i].w);
+        }
+        __syncthreads();
+        if (u + 1 < u1) issue(u + 1);  // K and V registers are free: the next chunk's loads go out
+        float scale[4], ls[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * g + r;
+            const float mc = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
+            const float mn = fmaxf(m_run[r], mc);
+            scale[r] = m_run[r] == -INFINITY ? 0.0f : __expf(m_run[r] - mn);
+            m_run[r] = mn;
+            const float pv = sc[r] == -INFINITY ? 0.0f : __expf(sc[r] - mn);
+            const uint32_t hi = f2bf(pv);
+            ps[0][h * kFaPStride + 16 * wave + l16] = (uint16_t)hi;
+            ps[1][h * kFaPStride + 16 * wave + l16] = (uint16_t)f2bf(pv - bf2f(hi));
+            ls[r] = pv;
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) ls[r] += __shfl_xor(ls[r], sh);
+        }
+        if (l16 == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red_l[wave][4 * g + r] = ls[r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * g + r;
+            l_run[r] = fmaf(l_run[r], scale[r], ((red_l[0][h] + red_l[1][h]) + red_l[2][h]) + red_l[3][h]);
+#pragma unroll
+            for (int dd = 0; dd < 2; ++dd) o[dd][r] *= scale[r];
+        }
+        // out[h][d] += sum_s p[h][s] v[s][d]: wave w takes dims 32 w .. 32 w + 31 of the block (two
+        // 16-column tiles), the 64 slots as two k steps of 32. A: weights of head l % 16, slots
+        // 32 kk + 8 (l / 16) .. + 7; B: V at those slots, dim l % 16 of the tile.
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const uint4 a = *reinterpret_cast<const uint4*>(ps[0] + l16 * kFaPStride + 32 * kk + 8 * g);
+            const uint4 al = *reinterpret_cast<const uint4*>(ps[1] + l16 * kFaPStride + 32 * kk + 8 * g);
+#pragma unroll
+            for (int dd = 0; dd < 2; ++dd) {
+                const int col = 32 * wave + 16 * dd + l16;
+                const uint16_t* vp = vs + (32 * kk + 8 * g) * kFaVStride + col;
+                uint32_t w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    w[i] = (uint32_t)vp[(2 * i) * kFaVStride] | ((uint32_t)vp[(2 * i + 1) * kFaVStride] << 16);
+                const bf16x8 bv = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
+                o[dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), bv, o[dd], 0, 0, 0);
+                o[dd] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(al), bv, o[dd], 0, 0, 0);
+            }
         }
     }
-    float* pc = part + ((size_t)m * kFaChunks + c) * kFaRec;
-    if (b == 0 && t < kGf) {
-        pc[t] = fmaxf(fmaxf(red_m[0][t], red_m[1][t]), fmaxf(red_m[2][t], red_m[3][t]));
-        pc[kGf + t] = ((red_l[0][t] + red_l[1][t]) + red_l[2][t]) + red_l[3][t];
+    float* pc = part + ((size_t)m * gridDim.x + blockIdx.x) * kFaRec;
+    if (b == 0 && l16 == 0 && wave == 0) {  // every wave holds the same per-head values
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pc[4 * g + r] = m_run[r];
+            pc[kGf + 4 * g + r] = l_run[r];
+        }
     }
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
@@ -195,7 +237,73 @@ __global__ __launch_bounds__(kFaBlock) void fattn_combine_kernel(const float* __
     }
 }
 
+// The fused pass (state from scratch): workgroup (h, b, m) merges the nrec records of row m for
+// head h, dims 128 b .. 128 b + 127. Wave w takes records w, w + 4, ...; lane l dims 2 l, 2 l + 1 of
+// the block. Records of chunks with no valid slot hold max -inf and add nothing.
+__global__ __launch_bounds__(kFaBlock) void fattn_merge_kernel(const float* __restrict__ part, int nrec, float* rmax,
+                                                               float* rsum, uint16_t* out) {
+    __shared__ float wm[4], wl[4];
+    __shared__ float2 wo[4][64];
+    const int h = blockIdx.x, b = blockIdx.y, m = blockIdx.z;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const float* pm = part + (size_t)m * nrec * kFaRec;
+    const int d = b * kFaDims + 2 * lane;
+    float mw = -INFINITY;
+    for (int x = wave; x < nrec; x += 4) mw = fmaxf(mw, pm[(size_t)x * kFaRec + h]);
+    if (lane == 0) wm[wave] = mw;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    if (mx != -INFINITY) {
+#pragma unroll 4
+        for (int x = wave; x < nrec; x += 4) {
+            const float* rec = pm + (size_t)x * kFaRec;
+            const float mr = rec[h];
+            const float f = mr == -INFINITY ? 0.0f : __expf(mr - mx);
+            l = fmaf(f, rec[kGf + h], l);
+            const float2 ov = *reinterpret_cast<const float2*>(rec + 2 * kGf + h * kDf + d);
+            o0 = fmaf(f, ov.x, o0);
+            o1 = fmaf(f, ov.y, o1);
+        }
+    }
+    if (lane == 0) wl[wave] = l;
+    wo[wave][lane] = make_float2(o0, o1);
+    __syncthreads();
+    if (wave != 0) return;
+    const float2 a = wo[0][lane], bq = wo[1][lane], c = wo[2][lane], e = wo[3][lane];
+    const size_t sh = (size_t)m * kGf + h;
+    *reinterpret_cast<uint32_t*>(out + sh * kDf + d) =
+        f2bf(((a.x + bq.x) + c.x) + e.x) | (f2bf(((a.y + bq.y) + c.y) + e.y) << 16);
+    if (b == 0 && lane == 0) {
+        rmax[sh] = mx;
+        rsum[sh] = ((wl[0] + wl[1]) + wl[2]) + wl[3];
+    }
+}
+
 }  // namespace
+
+hipError_t launch_full_attention(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                                 const float* masks, int P, float* running_max, float* running_sum, uint16_t* out,
+                                 int M, hipStream_t s, DevCtx* ctx) {
+    const int nchunks = P * kFaChunks;
+    const int cpw = (nchunks + kFaMaxRecords - 1) / kFaMaxRecords;  // chunks per workgroup
+    const int nrec = (nchunks + cpw - 1) / cpw;                      // records per row
+    const int rows = kFattnRecords / nrec;                           // rows per launch (scratch)
+    for (int m0 = 0; m0 < M; m0 += rows) {
+        const int mm = M - m0 < rows ? M - m0 : rows;
+        hipLaunchKernelGGL(fattn_partial_kernel, dim3(nrec, kFaDimBlocks, mm), dim3(kFaBlock), 0, s,
+                           q + (size_t)m0 * kQf, k_pages, v_pages, masks + (size_t)m0 * kTf, M * kTf, nchunks, cpw,
+                           ctx->fattn_part);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(fattn_merge_kernel, dim3(kGf, kFaDimBlocks, mm), dim3(kFaBlock), 0, s,
+                           (const float*)ctx->fattn_part, nrec, running_max + (size_t)m0 * kGf,
+                           running_sum + (size_t)m0 * kGf, out + (size_t)m0 * kQf);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
 
 hipError_t launch_full_attention_page(const uint16_t* q, const uint16_t* k_page, const uint16_t* v_page,
                                       const float* mask, float* running_max, float* running_sum, uint16_t* out,
@@ -203,7 +311,8 @@ hipError_t launch_full_attention_page(const uint16_t* q, const uint16_t* k_page,
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
         hipLaunchKernelGGL(fattn_partial_kernel, dim3(kFaChunks, kFaDimBlocks, mm), dim3(kFaBlock), 0, s,
-                           q + (size_t)m0 * kQf, k_page, v_page, mask + (size_t)m0 * kTf, ctx->fattn_part);
+                           q + (size_t)m0 * kQf, k_page, v_page, mask + (size_t)m0 * kTf, 0, kFaChunks, 1,
+                           ctx->fattn_part);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(fattn_combine_kernel, dim3(kGf, mm), dim3(kFaBlock), 0, s, (const float*)ctx->fattn_part,

@@ -44,7 +44,9 @@ constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (2 + k
 constexpr int kFaChunks = 8;
 constexpr int kFaDimBlocks = 4;
 constexpr int kFaRec = 2 * kGf + kGf * kDf;
-constexpr size_t kFattnPartFloats = (size_t)kMaxDecodeM * kFaChunks * kFaRec;
+constexpr int kFaMaxRecords = 64;                         // records per row of the fused pass
+constexpr int kFattnRecords = kMaxDecodeM * kFaChunks;     // 128 records of scratch
+constexpr size_t kFattnPartFloats = (size_t)kFattnRecords * kFaRec;
 
 // Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
 // never shared with another kernel).
@@ -133,6 +135,10 @@ hipError_t launch_full_o(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_full_attention_page(const uint16_t* q, const uint16_t* k_page, const uint16_t* v_page,
                                       const float* mask, float* running_max, float* running_sum, uint16_t* out,
                                       int M, bool first, hipStream_t s, DevCtx* ctx);
+// The state over pages 0 .. P - 1 (k_pages / v_pages [P][512][512], masks [P][M][512]) at once.
+hipError_t launch_full_attention(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages,
+                                 const float* masks, int P, float* running_max, float* running_sum, uint16_t* out,
+                                 int M, hipStream_t s, DevCtx* ctx);
 
 // MFMA path for one chunk of 1..kMaxChunkM token rows starting at row m0 of the call.
 hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);

@@ -64,6 +64,7 @@ SIGNATURES = {
     "moa_full_attention_first_page": [P] * 7 + [I32, P],
     "moa_full_attention_page": [P] * 7 + [I32, P],
     "moa_full_attention_output": [P] * 6 + [I32, P],
+    "moa_full_attention": [P] * 4 + [I32] + [P] * 3 + [I32, P],
     "moa_sliding_attention_output": [P] * 5 + [I32, P],
     "moa_sliding_attention_output_bf16_scales": [P] * 5 + [I32, P],
     "moa_decoder_feedforward": [P] * 13 + [I32, P],

@@ -136,6 +136,20 @@ def full_attention_page(q, k, v, mask, running_max, running_sum, out) -> None:
     _full_page("moa_full_attention_page", q, k, v, mask, running_max, running_sum, out)
 
 
+def full_attention(q, k_pages, v_pages, masks, running_max, running_sum, out) -> None:
+    """The state full_attention_first_page + full_attention_page over pages 1 .. P-1 leave, in two
+    launches: k_pages / v_pages [P, 512, 512] bf16 (contiguous), masks [P, M, 512] f32."""
+    M = _rows(q, QF, "q")
+    P = _rows(k_pages, TF * DF, "k_pages")
+    args = [
+        _ptr(q, "q", _BF16), _ptr(k_pages, "k_pages", _BF16), _ptr(v_pages, "v_pages", _BF16, P * TF * DF),
+        _ptr(masks, "masks", _F32, P * M * TF),
+    ]
+    tail = [_ptr(running_max, "running_max", _F32, M * GF), _ptr(running_sum, "running_sum", _F32, M * GF),
+            _ptr(out, "out", _BF16, M * QF)]
+    _lib.call("moa_full_attention", *args, P, *tail, M, _stream(q))
+
+
 def full_attention_output(x, running_sum, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
     """ops::full_attention_output (FO/src/ops.rs:176-199): x / running_sum, the O projection
     (K = 8192, bf16 per-row scales), post-norm and residual add, in place."""

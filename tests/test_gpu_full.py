@@ -205,3 +205,45 @@ def test_full_layer_attention_chain():
     assert ops.device_errors() == 0
     # residual + bf16(post-norm output): a one-ulp step of the addend may survive a cancellation
     gate_addend(w_res, g_res, o["residual"], "full layer chain residual")
+
+
+def fused_gpu(d):
+    from moa_amd import ops
+    P, M = d["masks"].shape[:2]
+    mx = torch.zeros(M * GF, dtype=torch.float32, device="cuda")
+    sm = torch.zeros(M * GF, dtype=torch.float32, device="cuda")
+    out = dev_zeros(M * QF)
+    ops.full_attention(dev(d["q"]), dev(d["k_pages"]), dev(d["v_pages"]), dev(d["masks"]), mx, sm, out)
+    return host(mx).reshape(M, GF), host(sm).reshape(M, GF), host(out).reshape(M, GF, DF)
+
+
+@pytest.mark.parametrize("P,M,q_std", [(1, 1, 1.0), (3, 2, 0.05), (8, 1, 1.0), (9, 2, 0.2), (64, 1, 0.05)])
+def test_fused_pages_match_oracle(P, M, q_std):
+    """moa_full_attention: all pages in two launches (spans of chunks with an online softmax for
+    P > 8). Its out is rounded to bf16 once, so the plain gate applies to the state itself."""
+    need_gpu()
+    say(f"full attention fused P={P} M={M} q_std={q_std}")
+    pos = [P * TF - 1] + [(P - 1) * TF + 37 * (m + 1) for m in range(1, M)]
+    d = synth.cfg_full_attention(seed=8, M=M, P=P, pos=pos, q_std=q_std)
+    gm, gs, go = fused_gpu(d)
+    wm, ws, wo = O.full_attention_pages(d["q"], d["k_pages"], d["v_pages"], d["masks"])
+    assert np.all(np.abs(gm - wm) <= 1e-3 * (1.0 + np.abs(wm))), "running_max"
+    assert np.all(np.abs(gs - ws) <= 1e-3 * np.abs(ws)), "running_sum"
+    gate(wo, go, f"fused P{P} out")
+
+
+def test_fused_pages_agree_with_the_per_page_calls():
+    need_gpu()
+    say("full attention: fused and per-page states, scattered masks and an empty row")
+    d = synth.cfg_full_attention(seed=9, M=3, P=4, q_std=0.3)
+    rng = np.random.default_rng(9)
+    d["masks"] = (rng.random(d["masks"].shape) < 0.3).astype(np.float32)
+    d["masks"][:, 2] = 0.0
+    fm, fs, fo = fused_gpu(d)
+    pm, ps, po = pages_gpu(d)
+    wm, ws, wo = O.full_attention_pages(d["q"], d["k_pages"], d["v_pages"], d["masks"])
+    assert np.all(fm[2] == -np.inf) and np.all(fs[2] == 0.0) and not fo[2].any()
+    assert np.array_equal(np.isfinite(fm), np.isfinite(pm))
+    gate(wo, fo, "fused scattered out")
+    fin = np.isfinite(wm)
+    assert np.all(np.abs(fm[fin] - pm[fin]) <= 1e-3 * (1.0 + np.abs(pm[fin])))
