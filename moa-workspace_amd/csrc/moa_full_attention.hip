@@ -248,22 +248,32 @@ __global__ __launch_bounds__(kFaBlock) void fattn_merge_kernel(const float* __re
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float* pm = part + (size_t)m * nrec * kFaRec;
     const int d = b * kFaDims + 2 * lane;
+    // every load of the wave's records is issued before any is used
+    constexpr int RW = kFaMaxRecords / 4;
+    float mr[RW], lr[RW];
+    float2 ov[RW];
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+        const int x = wave + 4 * i;
+        const float* rec = pm + (size_t)min(x, nrec - 1) * kFaRec;
+        mr[i] = x < nrec ? rec[h] : -INFINITY;
+        lr[i] = rec[kGf + h];
+        ov[i] = *reinterpret_cast<const float2*>(rec + 2 * kGf + h * kDf + d);
+    }
     float mw = -INFINITY;
-    for (int x = wave; x < nrec; x += 4) mw = fmaxf(mw, pm[(size_t)x * kFaRec + h]);
+#pragma unroll
+    for (int i = 0; i < RW; ++i) mw = fmaxf(mw, mr[i]);
     if (lane == 0) wm[wave] = mw;
     __syncthreads();
     const float mx = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
     float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
     if (mx != -INFINITY) {
-#pragma unroll 4
-        for (int x = wave; x < nrec; x += 4) {
-            const float* rec = pm + (size_t)x * kFaRec;
-            const float mr = rec[h];
-            const float f = mr == -INFINITY ? 0.0f : __expf(mr - mx);
-            l = fmaf(f, rec[kGf + h], l);
-            const float2 ov = *reinterpret_cast<const float2*>(rec + 2 * kGf + h * kDf + d);
-            o0 = fmaf(f, ov.x, o0);
-            o1 = fmaf(f, ov.y, o1);
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const float f = mr[i] == -INFINITY ? 0.0f : __expf(mr[i] - mx);
+            l = fmaf(f, lr[i], l);
+            o0 = fmaf(f, ov[i].x, o0);
+            o1 = fmaf(f, ov[i].y, o1);
         }
     }
     if (lane == 0) wl[wave] = l;
