@@ -60,7 +60,9 @@ BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          "fo": 3840 * 8192 + 3840 * 2 + 8192 * 2 + 16 * 4 + 3840 * 2 + 2 * 3840 * 2,
          "fattn": FATTN_PAGES * 2 * 512 * 512 * 2 + FATTN_PAGES * (8192 * 2 + 512 * 4 + 8192 * 2 * 2 + 16 * 4 * 4),
          # the same pages in one fused call: K, V, q, masks, the state written once
-         "fattn_fused": FATTN_PAGES * (2 * 512 * 512 * 2 + 512 * 4) + 8192 * 2 * 2 + 16 * 4 * 2}
+         "fattn_fused": FATTN_PAGES * (2 * 512 * 512 * 2 + 512 * 4) + 8192 * 2 * 2 + 16 * 4 * 2,
+         # the same at the cache's full 64 pages (position 32767)
+         "fattn_fused64": 64 * (2 * 512 * 512 * 2 + 512 * 4) + 8192 * 2 * 2 + 16 * 4 * 2}
 GRAPH_CALLS = 40  # calls per captured graph
 # Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
 FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
@@ -79,7 +81,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
-    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fo", "chunk"), default=None,
+    ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
+                             "chunk"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     args = ap.parse_args()
@@ -141,6 +144,10 @@ def main() -> int:
     fq_ro = torch.tensor([fq["rope_offset"]], dtype=torch.int32, device="cuda")
     fo_d = {k: dev(fo[k]) for k in ("x", "running_sum", "post_attn_rms_weight", "residual")}
     fa_q, fa_masks = dev(fa["q"]), dev(fa["masks"])
+    fa64 = synth.cfg_full_attention(1, M=1, P=64)
+    nfa64 = copies(BYTES["fattn_fused64"])
+    FAW64 = replicate(fa64, ("k_pages", "v_pages"), nfa64)
+    fa64_q, fa64_masks = dev(fa64["q"]), dev(fa64["masks"])
     fa_max = torch.zeros(16, dtype=torch.float32, device="cuda")
     fa_sum = torch.zeros(16, dtype=torch.float32, device="cuda")
     fa_out = torch.zeros(8192, dtype=torch.int16, device="cuda")
@@ -229,6 +236,10 @@ def main() -> int:
         w = FAW[i % nfa]
         ops.full_attention(fa_q, w["k_pages"], w["v_pages"], fa_masks, fa_max, fa_sum, fa_out)
 
+    def run_fattn_fused64(i):
+        w = FAW64[i % nfa64]
+        ops.full_attention(fa64_q, w["k_pages"], w["v_pages"], fa64_masks, fa_max, fa_sum, fa_out)
+
     def run_logits(i):
         ops.final_norm_and_logits(lg_in, lg_rms, lg_w, lg_out)
 
@@ -274,7 +285,8 @@ def main() -> int:
 
     if args.profile:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
-              "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused, "fo": run_fo,
+              "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
+              "fattn_fused64": run_fattn_fused64, "fo": run_fo,
               "chunk": run_layer}[args.profile]
         for i in range(args.steps):
             fn(i)
@@ -290,13 +302,13 @@ def main() -> int:
     per_op = {}
     for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn), ("logits", run_logits),
                      ("fqkv", run_fqkv), ("fattn", run_fattn), ("fattn_fused", run_fattn_fused),
-                     ("fo", run_fo)):
+                     ("fattn_fused64", run_fattn_fused64), ("fo", run_fo)):
         ms, _ = graph_timed(fn, args.steps, args.warmup)
         ms_host = timed(fn, min(args.steps, 50), 5)
         gbps = BYTES[name] / (ms * 1e-3) / 1e9
         per_op[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
                         "bytes": BYTES[name], "us_host_driven": round(ms_host * 1e3, 3)}
-        log(f"{name:11} {ms * 1e3:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / HBM_PEAK_GBPS:5.1f}% of 8 TB/s"
+        log(f"{name:13} {ms * 1e3:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / HBM_PEAK_GBPS:5.1f}% of 8 TB/s"
             f"   (host-driven {ms_host * 1e3:.2f} us)")
 
     ms_step, steps_done = graph_timed(run_step, args.steps, args.warmup)

@@ -44,8 +44,9 @@ constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (2 + k
 constexpr int kFaChunks = 8;
 constexpr int kFaDimBlocks = 4;
 constexpr int kFaRec = 2 * kGf + kGf * kDf;
-constexpr int kFaMaxRecords = 64;                         // records per row of the fused pass
-constexpr int kFattnRecords = kMaxDecodeM * kFaChunks;     // 128 records of scratch
+constexpr int kFaMaxRecords = 256;                        // records per row of the fused pass
+constexpr int kFaSplitPages = 8;                           // the fused pass splits dims up to 8 pages
+constexpr int kFattnRecords = 256;                         // records of scratch (>= kMaxDecodeM * kFaChunks)
 constexpr size_t kFattnPartFloats = (size_t)kFattnRecords * kFaRec;
 
 // Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
