@@ -59,3 +59,73 @@ def test_graph_replays_match_eager():
         torch.cuda.synchronize()
         assert np.array_equal(host(res), want[0])
     assert ops.device_errors() == 0
+
+
+def test_graph_replays_of_the_next_row_operators_match_eager():
+    """sliding_attention, the full-attention layer (QKV, pages per call and fused, output) and
+    final_norm_and_logits captured in one graph: every replay gives the eager bits."""
+    need_gpu()
+    from moa_amd import ops
+    ops.init(0)
+    at = synth.cfg_attention(3, M=1, pos=700)
+    A = {k: dev(at[k]) for k in ("q", "k_cache", "v_cache", "mask")}
+    a_out = torch.zeros(4096, dtype=torch.int16, device="cuda")
+    fq = synth.cfg_full_qkv(3, pos=1500)
+    F = {k: dev(fq[k]) for k in ("x", "q_weight", "k_weight", "q_weight_scale", "k_weight_scale", "input_rms_weight",
+                                 "q_rms_weight", "k_rms_weight", "cos", "sin")}
+    kv = torch.tensor([fq["kv_offset"]], dtype=torch.int32, device="cuda")
+    ro = torch.tensor([fq["rope_offset"]], dtype=torch.int32, device="cuda")
+    fa = synth.cfg_full_attention(3, M=1, P=12, q_std=0.3)
+    kp0, vp0 = dev(fa["k_pages"]), dev(fa["v_pages"])
+    kp, vp = kp0.clone(), vp0.clone()
+    masks = dev(fa["masks"])
+    q_f = torch.zeros(8192, dtype=torch.int16, device="cuda")
+    mx1, sm1, out1 = (torch.zeros(16, device="cuda"), torch.zeros(16, device="cuda"),
+                      torch.zeros(8192, dtype=torch.int16, device="cuda"))
+    mx2, sm2, out2 = (torch.zeros(16, device="cuda"), torch.zeros(16, device="cuda"),
+                      torch.zeros(8192, dtype=torch.int16, device="cuda"))
+    fo = synth.cfg_full_o(3)
+    O = {k: dev(fo[k]) for k in ("o_weight", "o_weight_scale", "post_attn_rms_weight")}
+    res0 = dev(fo["residual"])
+    res = res0.clone()
+    lg = synth.cfg_logits(3)
+    L = {k: dev(lg[k]) for k in ("input", "rms_weight")}
+    lm = synth.lm_head_device(3)
+    logits = torch.zeros(synth.W, dtype=torch.int16, device="cuda")
+
+    def step():
+        kp.copy_(kp0)
+        vp.copy_(vp0)
+        res.copy_(res0)
+        ops.sliding_attention(A["q"], A["k_cache"], A["v_cache"], A["mask"], a_out)
+        page = 1500 // 512
+        ops.full_project_qkv(F["x"], F["q_weight"], F["k_weight"], F["q_weight_scale"], F["k_weight_scale"],
+                             F["input_rms_weight"], F["q_rms_weight"], F["k_rms_weight"], kv, ro, F["cos"], F["sin"],
+                             kp[page], vp[page], q_f)
+        for p in range(12):
+            fn = ops.full_attention_first_page if p == 0 else ops.full_attention_page
+            fn(q_f, kp[p], vp[p], masks[p], mx1, sm1, out1)
+        ops.full_attention(q_f, kp, vp, masks, mx2, sm2, out2)
+        ops.full_attention_output(out2, sm2, O["post_attn_rms_weight"], O["o_weight"], O["o_weight_scale"], res)
+        ops.final_norm_and_logits(L["input"], L["rms_weight"], lm, logits)
+
+    outs = (a_out, kp, vp, q_f, mx1, sm1, out1, mx2, sm2, out2, res, logits)
+    names = ("attn", "k_pages", "v_pages", "q_f", "max", "sum", "out", "fused max", "fused sum", "fused out",
+             "residual", "logits")
+    step()
+    torch.cuda.synchronize()
+    assert ops.device_errors() == 0
+    want = [host(t).copy() for t in outs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for replay in range(3):
+        say(f"next-row graph replay {replay}")
+        for t in (a_out, q_f, out1, out2, logits):
+            t.fill_(0)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for w, t, name in zip(want, outs, names):
+            assert np.array_equal(w, host(t)), f"replay {replay}: {name} differs from the eager result"
+    assert ops.device_errors() == 0
