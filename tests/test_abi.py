@@ -44,6 +44,12 @@ def _null(n):
     ("moa_decoder_feedforward", 13, (1, None)),
     ("moa_decoder_feedforward_fp8", 10, (1, None)),
     ("moa_decoder_feedforward_mxfp4", 10, (1, None)),
+    ("moa_sliding_attention", 5, (1, None)),
+    ("moa_final_norm_and_logits", 4, (1, None)),
+    ("moa_full_project_qkv", 15, (1, None)),
+    ("moa_full_attention_first_page", 7, (1, None)),
+    ("moa_full_attention_page", 7, (1, None)),
+    ("moa_full_attention_output", 6, (1, None)),
 ])
 def test_null_pointers_rejected_on_host(fn, nptr, tail):
     lib = _lib.load()
@@ -72,6 +78,33 @@ def test_misaligned_and_bad_rows_rejected_on_host():
     assert rc == -1 and b"up_global_scale" in lib.moa_last_error_string()
     rc = lib.moa_decoder_feedforward_fp8(*([ok] * 5), None, ok, ok, None, None, 1, None)
     assert rc == -1 and b"up_weight_scale" in lib.moa_last_error_string()
+
+
+def test_next_row_entry_points_check_alignment_and_sizes_on_host():
+    lib = _lib.load()
+    buf = (C.c_uint8 * 4096)()
+    base = (C.addressof(buf) + 15) // 16 * 16
+    ok, bad2, bad4 = C.c_void_p(base), C.c_void_p(base + 2), C.c_void_p(base + 4)
+    # full attention: the page count must lie in [1, 64]
+    for P in (0, 65):
+        rc = lib.moa_full_attention(ok, ok, ok, ok, P, ok, ok, ok, 1, None)
+        assert rc == -1 and b"P must be" in lib.moa_last_error_string()
+    rc = lib.moa_full_attention(None, ok, ok, ok, 2, ok, ok, ok, 1, None)
+    assert rc == -1 and b"q is NULL" in lib.moa_last_error_string()
+    # 4-byte-aligned f32 state is enough; 16-byte tensors are not
+    rc = lib.moa_full_attention_page(ok, ok, ok, ok, bad2, ok, ok, 1, None)
+    assert rc == -2 and b"running_max" in lib.moa_last_error_string()
+    rc = lib.moa_full_attention_page(ok, ok, bad4, ok, ok, ok, ok, 1, None)
+    assert rc == -2 and b"v " in lib.moa_last_error_string()
+    rc = lib.moa_sliding_attention(ok, ok, ok, bad2, ok, 1, None)
+    assert rc == -2 and b"mask" in lib.moa_last_error_string()
+    rc = lib.moa_final_norm_and_logits(ok, ok, ok, ok, 0, None)
+    assert rc == -1 and b"M must be" in lib.moa_last_error_string()
+    # 2-byte-aligned bf16 scales pass the host checks; a 2-byte-aligned cos table does not
+    rc = lib.moa_full_project_qkv(*([ok] * 3), bad2, ok, *([ok] * 5), bad2, *([ok] * 4), 1, None)
+    assert rc == -2 and b"cos" in lib.moa_last_error_string()
+    rc = lib.moa_full_attention_output(ok, bad2, ok, ok, ok, ok, 1, None)
+    assert rc == -2 and b"running_sum" in lib.moa_last_error_string()
 
 
 def test_python_front_end_rejects_host_tensors():
