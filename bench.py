@@ -339,6 +339,10 @@ def main() -> int:
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(ffn, o, qkv, args.cpu_seconds)
+        lm_rows = lg_w[:LOGITS_CPU_ROWS].cpu().numpy().view(np.uint16)
+        for name, us, sample in cpu_next_ops(att, lg, lm_rows, fq, fa, fo):
+            per_op[name]["cpu_us"] = round(us, 1)
+            per_op[name]["cpu_sample"] = sample
 
     f = per_op["ffn"]
     # HBM bytes per FFN launch from the committed counter profile (FETCH_SIZE / WRITE_SIZE runs,
@@ -367,6 +371,48 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+LOGITS_CPU_ROWS = 16384  # vocabulary rows of the CPU logits sample (1/16 of the vocabulary)
+
+
+def cpu_next_ops(att, lg, lm_rows, fq, fa, fo, seconds: float = 1.0):
+    """The CPU oracle on the next-row operators' bench inputs: median wall time per call, about a
+    second of calls each (16 OpenMP threads). Logits: a sample of LOGITS_CPU_ROWS vocabulary rows,
+    scaled to the full 262144."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    def med(fn):
+        fn()
+        times, t_end = [], time.time() + seconds
+        while time.time() < t_end or len(times) < 3:
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        return float(np.median(times)) * 1e6
+
+    kp, vp, qo = fq["k_cache"].copy(), fq["v_cache"].copy(), np.zeros(8192, np.uint16)
+    unb = lambda b: (b.astype(np.uint32) << 16).view(np.float32)
+    res = fo["residual"].copy()
+    out = [
+        ("attn", med(lambda: O.sliding_attention(att["q"], att["k_cache"], att["v_cache"], att["mask"])),
+         "one call (M=1, 1024 slots)"),
+        ("logits", med(lambda: O.final_norm_and_logits(lg["input"], lg["rms_weight"], lm_rows)) * (262144 / len(lm_rows)),
+         f"{len(lm_rows)} vocabulary rows, scaled to 262144"),
+        ("fqkv", med(lambda: O.full_project_qkv(fq["x"], fq["q_weight"], fq["k_weight"], unb(fq["q_weight_scale"]),
+                                                unb(fq["k_weight_scale"]), fq["input_rms_weight"], fq["q_rms_weight"],
+                                                fq["k_rms_weight"], fq["kv_offset"], fq["rope_offset"], fq["cos"],
+                                                fq["sin"], kp, vp, qo)), "one call (M=1)"),
+        ("fattn_fused", med(lambda: O.full_attention_pages(fa["q"], fa["k_pages"], fa["v_pages"], fa["masks"])),
+         f"one call ({fa['masks'].shape[0]} pages)"),
+        ("fo", med(lambda: O.full_attention_output(fo["x"], fo["running_sum"], fo["post_attn_rms_weight"],
+                                                   fo["o_weight"], unb(fo["o_weight_scale"]), res)), "one call (M=1)"),
+    ]
+    for name, us, _ in out:
+        log(f"cpu oracle {name:11} {us:10.1f} us")
+    return out
 
 
 def cpu_baseline(ffn, o, qkv, seconds: float):
