@@ -28,7 +28,7 @@ namespace {
 constexpr int kAtBlock = 256;
 constexpr int kAtSlots = 32;                     // slots per workgroup
 constexpr int kAtChunks = kTs / kAtSlots;        // 32 workgroups per head
-constexpr int kAtPartFloats = 2 + kDs;           // max, sum, o[256]
+constexpr int kAtPartFloats = 4 + kDs;           // max, sum, 2 unused, o[256] (16-byte aligned)
 static_assert(kAtChunks == 32, "ticket arithmetic assumes 32 chunks per head");
 
 __device__ __forceinline__ float sc1_load(const float* p) {
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(kAtBlock) void attn_split_kernel(const uint16_t* __
         float o = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) o += ored[k][g][t];
-        sc1_store(mypart + g * kAtPartFloats + 2 + t, o);
+        sc1_store(mypart + g * kAtPartFloats + 4 + t, o);
         if (t < 2) sc1_store(mypart + g * kAtPartFloats + t, stat[g][t]);
     }
     // publish, then count the head's chunks; the workgroup completing the 32 combines them
@@ -153,32 +153,68 @@ __global__ __launch_bounds__(kAtBlock) void attn_split_kernel(const uint16_t* __
     __syncthreads();
     if (!s_last) return;
 
-    // combine: thread t owns dim t of both heads. Partials are read coherently (agent scope), every
-    // load of a thread issued before any is used.
+    // combine. Threads 0-63 read the 32 chunks' max and sum of both heads and turn them into the
+    // factors exp(max_c - max) and the head's sum. Every thread reads dims 4 q .. 4 q + 3
+    // (q = t % 64) of chunks 8 (t / 64) .. + 7 for both heads as 16-byte loads, all issued before
+    // any is used; the four chunk groups then meet in LDS in a fixed order. Partials are read
+    // coherently (agent scope: buffer loads with sc1, scalar atomic loads).
+    __shared__ float sf[kGs][kAtChunks], sl[kGs];
+    __shared__ float4 so[4][kGs][kDs / 4];
     const float* hp = part + ((size_t)m * kNs + n) * kAtChunks * kGs * kAtPartFloats;
-    float mc[kGs][kAtChunks], lc[kGs][kAtChunks], oc[kGs][kAtChunks];
+    const int q4 = t & 63, cg = t >> 6;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(hp), 0, (uint32_t)(kAtChunks * kGs * kAtPartFloats * sizeof(float)), 0x00020000);
+    float mcv = 0.0f, lcv = 0.0f;
+    if (t < 64) {  // first: the factors are computed while the outputs' loads are in flight
+        mcv = sc1_load(hp + ((t & 31) * kGs + (t >> 5)) * kAtPartFloats);
+        lcv = sc1_load(hp + ((t & 31) * kGs + (t >> 5)) * kAtPartFloats + 1);
+    }
+    float4 oc[kGs][8];
 #pragma unroll
     for (int g = 0; g < kGs; ++g)
 #pragma unroll
-        for (int cc = 0; cc < kAtChunks; ++cc) {
-            const float* pp = hp + (cc * kGs + g) * kAtPartFloats;
-            mc[g][cc] = sc1_load(pp);
-            lc[g][cc] = sc1_load(pp + 1);
-            oc[g][cc] = sc1_load(pp + 2 + t);
-        }
+        for (int i = 0; i < 8; ++i)
+            oc[g][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rs, (((cg * 8 + i) * kGs + g) * kAtPartFloats + 4 + 4 * q4) * 4,
+                                                      0, 16 /* sc1 */));
+    if (t < 64) {
+        const int g = t >> 5, cc = t & 31;
+        float mx = mcv;
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float f = mcv == -INFINITY ? 0.0f : __expf(mcv - mx);
+        float l = f * lcv;
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+        sf[g][cc] = f;
+        if (cc == 0) sl[g] = l;
+    }
+    __syncthreads();
 #pragma unroll
     for (int g = 0; g < kGs; ++g) {
-        float mx = -INFINITY;
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int cc = 0; cc < kAtChunks; ++cc) mx = fmaxf(mx, mc[g][cc]);
-        float l = 0.0f, o = 0.0f;
-#pragma unroll
-        for (int cc = 0; cc < kAtChunks; ++cc) {
-            const float f = mc[g][cc] == -INFINITY ? 0.0f : __expf(mc[g][cc] - mx);
-            l = fmaf(f, lc[g][cc], l);
-            o = fmaf(f, oc[g][cc], o);
+        for (int i = 0; i < 8; ++i) {
+            const float f = sf[g][cg * 8 + i];
+            a.x = fmaf(f, oc[g][i].x, a.x);
+            a.y = fmaf(f, oc[g][i].y, a.y);
+            a.z = fmaf(f, oc[g][i].z, a.z);
+            a.w = fmaf(f, oc[g][i].w, a.w);
         }
-        out[(((size_t)m * kNs + n) * kGs + g) * kDs + t] = (uint16_t)f2bf(l > 0.0f ? o / l : 0.0f);
+        so[cg][g][q4] = a;
+    }
+    __syncthreads();
+    if (t < kGs * 64) {
+        const int g = t >> 6, q = t & 63;
+        const float l = sl[g];
+        const float4 a = so[0][g][q], b = so[1][g][q], c2 = so[2][g][q], d = so[3][g][q];
+        float v[4] = {((a.x + b.x) + c2.x) + d.x, ((a.y + b.y) + c2.y) + d.y, ((a.z + b.z) + c2.z) + d.z,
+                      ((a.w + b.w) + c2.w) + d.w};
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f2bf(l > 0.0f ? v[e] / l : 0.0f);
+        *reinterpret_cast<uint2*>(out + (((size_t)m * kNs + n) * kGs + g) * kDs + 4 * q) =
+            make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
     }
 }
 

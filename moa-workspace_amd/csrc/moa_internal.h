@@ -39,7 +39,7 @@ constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN wo
 constexpr int kTicketAttn = kTicketFfnEpoch + 16;
 constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;
 // sliding_attention partials: [kMaxDecodeM][kNs][32 chunks][kGs][max, sum, o[kDs]]
-constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (2 + kDs);
+constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (4 + kDs);
 // full-attention page partials: per token row and 64-slot chunk, 16 maxima, 16 sums, out [16][512]
 constexpr int kFaChunks = 8;
 constexpr int kFaDimBlocks = 4;
