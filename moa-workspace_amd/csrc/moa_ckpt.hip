@@ -302,12 +302,38 @@ class Json {
     }
 };
 
+// The header is JSON, so UTF-8: every byte sequence must be a well-formed UTF-8 character (no
+// overlong forms, no surrogates, nothing above U+10FFFF), as a JSON reader of the format requires.
+bool valid_utf8(const uint8_t* p, size_t n) {
+    size_t i = 0;
+    while (i < n) {
+        const uint8_t b = p[i];
+        if (b < 0x80) { ++i; continue; }
+        int len;
+        uint32_t cp;
+        if ((b & 0xE0) == 0xC0) { len = 2; cp = b & 0x1F; }
+        else if ((b & 0xF0) == 0xE0) { len = 3; cp = b & 0x0F; }
+        else if ((b & 0xF8) == 0xF0) { len = 4; cp = b & 0x07; }
+        else return false;
+        if (i + len > n) return false;
+        for (int k = 1; k < len; ++k) {
+            if ((p[i + k] & 0xC0) != 0x80) return false;
+            cp = (cp << 6) | (p[i + k] & 0x3F);
+        }
+        static const uint32_t kMin[5] = {0, 0, 0x80, 0x800, 0x10000};
+        if (cp < kMin[len] || cp > 0x10FFFF || (cp >= 0xD800 && cp < 0xE000)) return false;
+        i += len;
+    }
+    return true;
+}
+
 int parse(moa_ckpt* c) {
     if (c->size < 8) return err(MOA_ERROR_FORMAT, c->path + ": shorter than the 8-byte header length");
     uint64_t n = 0;
     for (int i = 7; i >= 0; --i) n = (n << 8) | c->map[i];
     if (n > kMaxHeader) return err(MOA_ERROR_FORMAT, c->path + ": header length " + std::to_string(n) + " too large");
     if (n > c->size - 8) return err(MOA_ERROR_FORMAT, c->path + ": header runs past the end of the file");
+    if (!valid_utf8(c->map + 8, (size_t)n)) return err(MOA_ERROR_FORMAT, c->path + ": header is not valid UTF-8");
     Json j(reinterpret_cast<const char*>(c->map + 8), (size_t)n);
     if (!j.header(c)) return err(MOA_ERROR_FORMAT, c->path + ": " + j.error);
     c->data = c->map + 8 + n;

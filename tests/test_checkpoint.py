@@ -142,6 +142,8 @@ def _entry(dtype="U8", shape=(4,), offsets=(0, 4)):
     (_file(_entry() + b"x", b"abcd"), "trailing bytes"),
     (_file(b'{"t":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}', b"abcd"), "expected ',' or '}'"),
     (_file(b'{"t\\q":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', b"abcd"), "bad escape"),
+    (_file(b'{"t\xc3":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', b"abcd"), "not valid UTF-8"),
+    (_file(b'{"t\xed\xa0\x80":{"dtype":"U8","shape":[4],"data_offsets":[0,4]}}', b"abcd"), "not valid UTF-8"),
 ])
 def test_malformed_files_are_rejected(tmp_path, blob, needle):
     p = tmp_path / "bad.safetensors"
@@ -200,3 +202,37 @@ def test_model_dir_resolution(tmp_path, monkeypatch):
 def test_layer_pattern():
     full = [i for i in range(checkpoint.LAYERS) if checkpoint.is_full_layer(i)]
     assert full == [5, 11, 17, 23, 29, 35, 41, 47]
+
+
+def test_mutated_headers_are_parsed_or_rejected_never_crash(ckfile, tmp_path):
+    """Random byte flips, insertions and deletions in the JSON header of a valid file: every
+    result is a clean open (the bytes still form a valid header) or MOA_ERROR_FORMAT."""
+    p, _ = ckfile
+    blob = p.read_bytes()
+    n = struct.unpack("<Q", blob[:8])[0]
+    header, data = bytearray(blob[8:8 + n]), blob[8 + n:]
+    rng = np.random.default_rng(1234)
+    q = tmp_path / "mut.safetensors"
+    opened = rejected = 0
+    for _ in range(300):
+        h = bytearray(header)
+        for _ in range(int(rng.integers(1, 4))):
+            at = int(rng.integers(0, len(h)))
+            kind = int(rng.integers(0, 3))
+            if kind == 0:
+                h[at] = int(rng.integers(0, 256))
+            elif kind == 1:
+                h.insert(at, int(rng.choice(list(b'{}[],:"\\\\0123456789 eE-.u'))))
+            elif len(h) > 2:
+                del h[at]
+        q.write_bytes(struct.pack("<Q", len(h)) + bytes(h) + data)
+        try:
+            with checkpoint.Checkpoint(q) as ck:
+                for name in ck.names():
+                    dt, shape, nb = ck.info(name)
+                    assert len(ck.read(name)) == nb
+            opened += 1
+        except _lib.MoaError as e:
+            assert e.code == FORMAT, str(e)
+            rejected += 1
+    assert rejected > 100
