@@ -79,6 +79,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample length (0 = skip)")
+    ap.add_argument("--ckpt-gib", type=float, default=1.0,
+                    help="size of the synthetic checkpoint file the loader is timed on (0 = skip)")
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
@@ -328,6 +330,10 @@ def main() -> int:
             log(f"chunk M={CM} {name:5} {ms * 1e3:9.2f} us  {tf:7.1f} TFLOP/s  "
                 f"{100 * tf / MFMA_BF16_PEAK_TFLOPS:5.1f}% of bf16 MFMA peak")
 
+    ckpt = ckpt_measure(args.ckpt_gib) if args.ckpt_gib > 0 else None
+    if ckpt:
+        ckpt["file_GiB"] = args.ckpt_gib
+
     # attainable HBM bandwidth: device-to-device copy of 2 GiB (read + write)
     big = torch.empty(1 << 30, dtype=torch.int16, device="cuda")
     dst = torch.empty_like(big)
@@ -367,10 +373,64 @@ def main() -> int:
         "us_per_token_host_driven": round(ms_step_host * 1e3, 3),
         "hbm_copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": cpu,
+        "checkpoint_load": ckpt,
         "chunk": chunk,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def ckpt_measure(gib: float = 1.0):
+    """The checkpoint reader (moa_ckpt_load_bf16) on a synthetic one-tensor safetensors file of
+    `gib` GiB, already in the page cache: host-to-device GB/s, median of 3 loads, beside a plain
+    pinned-memory copy of the same size (torch) as the link's attainable rate."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from moa_amd import checkpoint
+
+    rows = int(gib * 2**30) // (3840 * 2)
+    nbytes = rows * 3840 * 2
+    hdr = json.dumps({"t": {"dtype": "BF16", "shape": [rows, 3840], "data_offsets": [0, nbytes]}}).encode()
+    hdr += b" " * (-len(hdr) % 8)
+    d = tempfile.mkdtemp(dir=os.environ.get("TMPDIR"))
+    path = os.path.join(d, "model.safetensors")
+    chunk = np.random.default_rng(0).integers(0, 1 << 16, size=(64 << 20) // 2, dtype=np.uint16).tobytes()
+    with open(path, "wb") as f:
+        f.write(len(hdr).to_bytes(8, "little") + hdr)
+        left = nbytes
+        while left:
+            f.write(chunk[: min(left, len(chunk))])
+            left -= min(left, len(chunk))
+    try:
+        times = []
+        with checkpoint.Checkpoint(path) as ck:
+            for _ in range(4):
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                x = ck.load_bf16("t", (rows, 3840))
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t)
+                del x
+        pinned = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        ptimes = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            dst.copy_(pinned, non_blocking=True)
+            torch.cuda.synchronize()
+            ptimes.append(time.perf_counter() - t)
+        del pinned, dst
+    finally:
+        os.remove(path)
+        os.rmdir(d)
+    gbps = nbytes / float(np.median(times[1:])) / 1e9
+    link = nbytes / float(np.median(ptimes)) / 1e9
+    log(f"checkpoint load {gbps:7.1f} GB/s (pinned host-to-device copy {link:.1f} GB/s)")
+    return {"GBps": round(gbps, 1), "pinned_copy_GBps": round(link, 1), "bytes": nbytes}
 
 
 LOGITS_CPU_ROWS = 16384  # vocabulary rows of the CPU logits sample (1/16 of the vocabulary)
