@@ -17,9 +17,9 @@
 // Two launches per page:
 //  1. fattn_partial_kernel, grid (8 slot chunks, 4 dim blocks, M): workgroup (c, b, m) scores the
 //     64 slots of chunk c against all 16 heads on the matrix cores (v_mfma_f32_16x16x32_bf16: the
-//     heads as A rows, K rows as B columns, each wave a quarter of the 512 dims), takes each head's max and the
-//     f32 exp weights, and multiplies them into its 128 dims of V (V staged through LDS, where the
-//     B operand's slot-major gather is cheap). A weight enters the MFMA as two bf16 parts, high
+//     heads as A rows, K rows as B columns, each wave a quarter of the 512 dims), takes each
+//     head's max and the f32 exp weights, and multiplies them into its 128 dims of V (V staged
+//     through LDS, where the B operand's slot-major gather is cheap). A weight enters the MFMA as two bf16 parts, high
 //     and low (about 16 significant bits; one bf16 part alone would put a 2^-9 relative error on
 //     every weight). It writes the chunk's per-head max, sum and partial out (f32).
 //  2. fattn_combine_kernel, grid (16 heads, M): merges the 8 chunks with the old state and writes

@@ -27,7 +27,8 @@ def run_oracle(d):
     return O.sliding_attention(d["q"], d["k_cache"], d["v_cache"], d["mask"])
 
 
-@pytest.mark.parametrize("q_std,pos", [(1.0, 5000), (1.0, 1023), (1.0, 0), (1.0, 1), (0.1, 511), (0.1, 5000), (0.3, 31)])
+@pytest.mark.parametrize("q_std,pos", [(1.0, 5000), (1.0, 1023), (1.0, 0), (1.0, 1), (0.1, 511), (0.1, 5000), (0.3, 31),
+                                       (8.0, 5000)])
 def test_matches_oracle(q_std, pos):
     need_gpu()
     say(f"attention q_std={q_std} pos={pos}")

@@ -217,7 +217,8 @@ def fused_gpu(d):
     return host(mx).reshape(M, GF), host(sm).reshape(M, GF), host(out).reshape(M, GF, DF)
 
 
-@pytest.mark.parametrize("P,M,q_std", [(1, 1, 1.0), (3, 2, 0.05), (8, 1, 1.0), (9, 2, 0.2), (64, 1, 0.05)])
+@pytest.mark.parametrize("P,M,q_std", [(1, 1, 1.0), (3, 2, 0.05), (8, 1, 1.0), (9, 2, 0.2), (64, 1, 0.05),
+                                       (12, 1, 6.0)])
 def test_fused_pages_match_oracle(P, M, q_std):
     """moa_full_attention: all pages in two launches (spans of chunks with an online softmax for
     P > 8). Its out is rounded to bf16 once, so the plain gate applies to the state itself."""
