@@ -13,7 +13,8 @@
  *   - stream is a hipStream_t (NULL = the null stream); all work is ordered on it and the
  *     call returns without synchronising. Calls on one device must be issued from one
  *     stream at a time: the per-device scratch is shared.
- * Pointers must be 16-byte aligned except per-channel scales (natural alignment).
+ * Pointers must be 16-byte aligned except per-channel scales (natural alignment) and FP4
+ * block-scale codes (4-byte aligned).
  *
  * Return value: MOA_SUCCESS or a negative MOA_ERROR_* code; moa_last_error_string() gives
  * the reason. Invalid arguments are rejected before anything is launched. Device-resident

@@ -21,7 +21,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libmoa_gfx950.so"
-SOURCES = ["moa_api.hip", "moa_decode.hip", "moa_chunk.hip", "moa_attention.hip", "moa_logits.hip", "moa_ckpt.hip", "moa_full_attention.hip"]
+SOURCES = ["moa_api.hip", "moa_decode.hip", "moa_chunk.hip", "moa_attention.hip", "moa_logits.hip", "moa_ckpt.hip", "moa_full_attention.hip", "moa_rows.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

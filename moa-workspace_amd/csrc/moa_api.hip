@@ -180,7 +180,7 @@ int ffn_common(const FfnParams& p, int M, void* stream) {
         const size_t sa = p.scale_kind == ScaleKind::F32 ? 4 : 2;
         c.ptr(p.up_s, "up_weight_scale", sa).ptr(p.gate_s, "gate_weight_scale", sa).ptr(p.down_s, "down_weight_scale", sa);
     } else {
-        const size_t sa = p.fmt == FfnFormat::NVFP4 ? 2 : 1;
+        const size_t sa = 4;  // FP4 block-scale codes: read a dword at a time
         c.ptr(p.up_s, "up_weight_scale", sa).ptr(p.gate_s, "gate_weight_scale", sa).ptr(p.down_s, "down_weight_scale", sa);
     }
     if (p.fmt == FfnFormat::NVFP4) {

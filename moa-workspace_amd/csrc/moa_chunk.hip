@@ -344,8 +344,9 @@ __device__ __forceinline__ float ck_block_sum(float v, float* red) {
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
-// out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) (gemma4.py:83-89), written as A tiles.
-// One workgroup per row; thread t < 240 owns elements 16t .. 16t+15.
+// out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) (gemma4.py:83-89), written as A tiles
+// (Tiles) or row-major [M][kH]. One workgroup per row; thread t < 240 owns elements 16t .. 16t+15.
+template <bool Tiles = true>
 __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint16_t* __restrict__ x,
                                                                       const uint16_t* __restrict__ w,
                                                                       uint16_t* __restrict__ out) {
@@ -370,8 +371,10 @@ __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
-    *reinterpret_cast<uint4*>(out + atile_off(m, c * 16, kH)) = make_uint4(h[0], h[1], h[2], h[3]);
-    *reinterpret_cast<uint4*>(out + atile_off(m, c * 16 + 8, kH)) = make_uint4(h[4], h[5], h[6], h[7]);
+    const size_t o0 = Tiles ? atile_off(m, c * 16, kH) : (size_t)m * kH + c * 16;
+    const size_t o1 = Tiles ? atile_off(m, c * 16 + 8, kH) : (size_t)m * kH + c * 16 + 8;
+    *reinterpret_cast<uint4*>(out + o0) = make_uint4(h[0], h[1], h[2], h[3]);
+    *reinterpret_cast<uint4*>(out + o1) = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
 // Row-major bf16 [M][K] -> A tiles (the O-projection's input arrives row-major). One workgroup
@@ -441,15 +444,25 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
 // Per row: d = bf16((sum of the split-K partials) * s[n]), then out = bf16(bf16(r + N(d)) * ls)
 // with N the post-RMSNorm (identity when w_post is null) and ls skipped when null
 // (shared/rmsnorm.rs:204-296, residual.rs:189-241; generate_references.py:411-413).
-template <ScaleKind SK>
+template <ScaleKind SK, FfnFormat F = FfnFormat::FP8>
 __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* __restrict__ part, int splits, int M,
-                                                                   const void* scale, const uint16_t* __restrict__ w_post,
+                                                                   const void* scale, const float* __restrict__ gscale,
+                                                                   const uint16_t* __restrict__ w_post,
                                                                    uint16_t* __restrict__ res, const uint16_t* __restrict__ ls) {
     __shared__ float red[4];
     const int t = threadIdx.x, m = blockIdx.x;
+    const float gs = F == FfnFormat::NVFP4 ? *gscale : 1.0f;
     constexpr int NC = kH / 8;  // 480 chunks of 8; thread t owns t and t + 256
     float d[2][8];
     float ss = 0.0f;
+    // the residual and post-norm weight chunks are loaded first, in flight during the partial sums
+    uint4 rq[2], wq[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = min(t + 256 * i, NC - 1);
+        rq[i] = ld16(res + (size_t)m * kH + c * 8);
+        wq[i] = w_post ? ld16(w_post + c * 8) : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = min(t + 256 * i, NC - 1);
@@ -473,7 +486,10 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            d[i][e] = rbf(a[e] * chunk_scale<SK>(scale, c * 8 + e));
+            // the format's commit: FP8 bf16(sum * s[n]); NVFP4 bf16(bf16(sum) * 1/g); MXFP4 bf16(sum)
+            if constexpr (F == FfnFormat::FP8) d[i][e] = rbf(a[e] * chunk_scale<SK>(scale, c * 8 + e));
+            else if constexpr (F == FfnFormat::NVFP4) d[i][e] = rbf(rbf(a[e]) * gs);
+            else d[i][e] = rbf(a[e]);
             if (act) ss = fmaf(d[i][e], d[i][e], ss);
         }
     }
@@ -485,8 +501,8 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
         if (c >= NC) continue;
         uint16_t* rr = res + (size_t)m * kH + c * 8;
         float rv[8], wv[8];
-        bf16x8_to_f32(ld16(rr), rv);
-        if (w_post) bf16x8_to_f32(ld16(w_post + c * 8), wv);
+        bf16x8_to_f32(rq[i], rv);
+        bf16x8_to_f32(wq[i], wv);
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -535,13 +551,13 @@ int m_tiles(int M) { return (M + kCkBM - 1) / kCkBM; }
 template <ScaleKind SK>
 hipError_t post_rows(const float* part, int splits, int M, const void* scale, const uint16_t* w_post, uint16_t* res,
                      const uint16_t* ls, hipStream_t s) {
-    return ck_launch(chunk_post_rows_kernel<SK>, dim3(M), s, part, splits, M, scale, w_post, res, ls);
+    return ck_launch(chunk_post_rows_kernel<SK>, dim3(M), s, part, splits, M, scale, (const float*)nullptr, w_post, res, ls);
 }
 
 }  // namespace
 
 hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
-    hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel, dim3(M), s, p.x + (size_t)m0 * kH, p.in_rms, ctx->hbuf);
+    hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel<true>, dim3(M), s, p.x + (size_t)m0 * kH, p.in_rms, ctx->hbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
     g.x = ctx->hbuf; g.M = M; g.N = kQkvRowsTotal; g.K = kH;
@@ -575,7 +591,7 @@ hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx
 hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
     if (p.fmt != FfnFormat::FP8) return hipErrorInvalidValue;
     uint16_t* res = p.residual + (size_t)m0 * kH;
-    hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel, dim3(M), s, (const uint16_t*)res, p.pre_rms, ctx->hbuf);
+    hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel<true>, dim3(M), s, (const uint16_t*)res, p.pre_rms, ctx->hbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
     g.x = ctx->hbuf; g.M = M; g.N = kL; g.K = kH;
@@ -593,6 +609,25 @@ hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, De
     return p.scale_kind == ScaleKind::F32
         ? post_rows<ScaleKind::F32>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s)
         : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
+}
+
+hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, hipStream_t s) {
+    return ck_launch(chunk_rmsnorm_rows_kernel<false>, dim3(M), s, x, w, out);
+}
+
+hipError_t launch_ffn_post_rows(const FfnParams& p, const float* part, int splits, int M, uint16_t* res, hipStream_t s) {
+    switch (p.fmt) {
+        case FfnFormat::FP8:
+            return p.scale_kind == ScaleKind::F32 ? post_rows<ScaleKind::F32>(part, splits, M, p.down_s, p.post_rms, res, p.layer_scalar, s)
+                                                  : post_rows<ScaleKind::BF16>(part, splits, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
+        case FfnFormat::NVFP4:
+            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::NVFP4>, dim3(M), s, part, splits, M,
+                             (const void*)nullptr, p.down_g, p.post_rms, res, p.layer_scalar);
+        case FfnFormat::MXFP4:
+            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::MXFP4>, dim3(M), s, part, splits, M,
+                             (const void*)nullptr, (const float*)nullptr, p.post_rms, res, p.layer_scalar);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace moa

@@ -18,6 +18,7 @@
 
 #include "moa_device.h"
 #include "moa_internal.h"
+#include "moa_sync.h"
 
 namespace moa {
 namespace {
@@ -31,41 +32,6 @@ template <ScaleKind SK>
 __device__ __forceinline__ float load_scale(const void* p, int i) {
     if constexpr (SK == ScaleKind::F32) return static_cast<const float*>(p)[i];
     else return bf2f(static_cast<const uint16_t*>(p)[i]);
-}
-
-// Cross-workgroup hand-off for the grid-wide epilogues.
-//
-// Workgroups publish() their results and then arrive on device-scope counters; the workgroup
-// that arrives last reads every result with collect(). Results are agent-scope atomic
-// stores/loads (global_store/load sc1 on gfx950: coherent across the XCDs' L2s without cache
-// maintenance). Each wave waits for its own stores to complete (s_waitcnt vmcnt(0)) before its
-// workgroup arrives, so a value is visible once the counters have counted its workgroup. No L2
-// writeback/invalidate is issued (a fence per wave costs more than these kernels' weight
-// stream), and each workgroup arrives once, on counters that never share a 256-byte line:
-// device-scope atomics to one line serialise. Counters reset themselves, so consecutive launches
-// on one stream reuse them.
-__device__ __forceinline__ void publish(uint16_t* p, uint32_t v) {
-    __hip_atomic_store(p, (uint16_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint32_t collect(const uint16_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Eight published bf16 values (16 bytes) read coherently.
-__device__ __forceinline__ uint4 collect16(const uint16_t* p) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    return make_uint4(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                      __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                      __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                      __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
-__device__ __forceinline__ uint32_t counter_add(uint32_t* c) {
-    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void counter_reset(uint32_t* c) {
-    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Whole block: true in every thread of the block that arrives last of `expected` on `ctr`.
@@ -106,26 +72,6 @@ __device__ __forceinline__ bool block_arrive_tree(uint32_t* tree, uint32_t nbloc
     __syncthreads();
     return s_last;
 }
-
-// Tagged hand-off (single-launch kernels). A 64-bit word carries a value in its low half and the
-// launch's tag in its high half, written by one agent-scope store: a reader that sees the tag has
-// the whole value, so no counter has to follow the data. Tags come from monotonic counters (a
-// launch's epoch), so words left by an earlier launch never carry the current tag.
-constexpr uint64_t kSpinTicks = 1ull << 24;  // bound of every poll: ~168 ms of the 100 MHz wall clock
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void glb_void;
-
-__device__ __forceinline__ void publish32(void* p, uint32_t v) {
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void publish64(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t collect64(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
 
 // Post-norm hand-off of the single-launch O and FFN kernels (240 workgroups of 16 output rows):
 // per workgroup one partial sum of squares (f32 bits) and eight words of two bf16 outputs.
@@ -1306,32 +1252,6 @@ __device__ __forceinline__ void reload_stale(uint64_t (&w)[N], uint32_t tag, A a
     ((w[I] = (uint32_t)(w[I] >> 32) != tag ? collect64(addr(I)) : w[I]), ...);
 }
 
-// One lane per workgroup, after its workgroup's results are published and complete: arrive on
-// `tree` (kTreeCounters counters kTicketStride apart) and wait until `gen` reads `target`.
-__device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint32_t target, uint32_t* err) {
-    const uint32_t leaf = blockIdx.x % kTreeLeaves;
-    const uint32_t n_leaf = (gridDim.x - leaf + kTreeLeaves - 1) / kTreeLeaves;
-    const uint32_t n_root = gridDim.x < (uint32_t)kTreeLeaves ? gridDim.x : (uint32_t)kTreeLeaves;
-    uint32_t* lc = tree + leaf * kTicketStride;
-    if (counter_add(lc) + 1u == n_leaf) {
-        counter_reset(lc);
-        uint32_t* rc = tree + kTreeLeaves * kTicketStride;
-        if (counter_add(rc) + 1u == n_root) {
-            counter_reset(rc);
-            __hip_atomic_store(gen, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    const uint64_t t0 = wall_clock64();
-    while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target) {
-        if (wall_clock64() - t0 > kSpinTicks) {
-            atomicOr(err, kErrSpinTimeout);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-}
-
-
 template <FfnFormat F, ScaleKind SK>
 __global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostSlots* slots, uint32_t* tickets,
@@ -1678,10 +1598,9 @@ static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevC
             if (e != hipSuccess) return e;
             continue;
         }
-        e = launch(ffn_up_gate_kernel<F, SK>, dim3(kL / (4 * kUgRL), mm), s, p, m0, ctx->pbuf);
-        if (e != hipSuccess) return e;
-        e = launch(ffn_down_kernel<F, SK>, dim3(kH / (4 * kDownR), mm), s, p, m0,
-                   (const uint16_t*)ctx->pbuf, ctx->dbuf, ctx->tickets);
+        // 2..16 rows (or one row whose single-launch grid does not fit): the matrix-core path,
+        // which reads each weight once for all rows
+        e = launch_ffn_rows(p, m0, mm, s, ctx);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

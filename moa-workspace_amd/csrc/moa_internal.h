@@ -37,7 +37,10 @@ constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
 constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN workgroups each
 // sliding_attention: one counter per (row, head) of a launch, 32 arrivals per launch, never reset
 constexpr int kTicketAttn = kTicketFfnEpoch + 16;
-constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;
+// grid barrier of the single-launch FFN for 2..16 rows (moa_rows.hip): a 17-counter tree and a generation word
+constexpr int kTicketRowsBar = kTicketAttn + kMaxDecodeM * kNs;
+constexpr int kTicketRowsGen = kTicketRowsBar + kTreeCounters;
+constexpr int kTicketCount = kTicketRowsGen + 1;
 // sliding_attention partials: [kMaxDecodeM][kNs][32 chunks][kGs][max, sum, o[kDs]]
 constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (4 + kDs);
 // full-attention page partials: per token row and 64-slot chunk, 16 maxima, 16 sums, out [16][512]
@@ -82,6 +85,7 @@ struct DevCtx {
     int8_t o_fused[2] = {-1, -1};                    // per scale kind
     int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
     int8_t full_o_fused[2] = {-1, -1};               // the same for full_attention_output
+    int8_t rows_fused[6] = {-1, -1, -1, -1, -1, -1}; // per (format, scale kind): single-launch rows FFN fits?
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
@@ -145,6 +149,13 @@ hipError_t launch_full_attention(const uint16_t* q, const uint16_t* k_pages, con
 hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);  // FP8 weights
+// decoder_feedforward for 1..kMaxDecodeM rows on the matrix cores (every format; moa_rows.hip), and its
+// last step: the sum of `splits` f32 partials [splits][M][kH] of the down projection, the format's
+// commit, post-RMSNorm, residual and layer scalar into res [M][kH].
+hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_ffn_post_rows(const FfnParams& p, const float* part, int splits, int M, uint16_t* res, hipStream_t s);
+// out[m] = bf16(RMSNorm(x[m]) * w) for M rows of kH, row-major (gemma4.py:83-89).
+hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, hipStream_t s);
 
 // ops::final_norm_and_logits for M token rows (input [M][kH], out [M][kW]).
 hipError_t launch_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_w, const uint16_t* w, uint16_t* out,

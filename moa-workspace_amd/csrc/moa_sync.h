@@ -1,0 +1,91 @@
+// moa_sync.h -- cross-workgroup hand-off primitives shared by the single-launch kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moa_internal.h"
+
+namespace moa {
+
+// Cross-workgroup hand-off for the grid-wide epilogues.
+//
+// Workgroups publish() their results and then arrive on device-scope counters; the workgroup
+// that arrives last reads every result with collect(). Results are agent-scope atomic
+// stores/loads (global_store/load sc1 on gfx950: coherent across the XCDs' L2s without cache
+// maintenance). Each wave waits for its own stores to complete (s_waitcnt vmcnt(0)) before its
+// workgroup arrives, so a value is visible once the counters have counted its workgroup. No L2
+// writeback/invalidate is issued (a fence per wave costs more than these kernels' weight
+// stream), and each workgroup arrives once, on counters that never share a 256-byte line:
+// device-scope atomics to one line serialise. Counters reset themselves, so consecutive launches
+// on one stream reuse them.
+__device__ __forceinline__ void publish(uint16_t* p, uint32_t v) {
+    __hip_atomic_store(p, (uint16_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t collect(const uint16_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Eight published bf16 values (16 bytes) read coherently.
+__device__ __forceinline__ uint4 collect16(const uint16_t* p) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return make_uint4(__hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                      __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ uint32_t counter_add(uint32_t* c) {
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void counter_reset(uint32_t* c) {
+    __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tagged hand-off (single-launch kernels). A 64-bit word carries a value in its low half and the
+// launch's tag in its high half, written by one agent-scope store: a reader that sees the tag has
+// the whole value, so no counter has to follow the data. Tags come from monotonic counters (a
+// launch's epoch), so words left by an earlier launch never carry the current tag.
+constexpr uint64_t kSpinTicks = 1ull << 24;  // bound of every poll: ~168 ms of the 100 MHz wall clock
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+__device__ __forceinline__ void publish32(void* p, uint32_t v) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t collect64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
+
+// One lane per workgroup, after its workgroup's results are published and complete: arrive on
+// `tree` (kTreeCounters counters kTicketStride apart) and wait until `gen` reads `target`.
+__device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint32_t target, uint32_t* err) {
+    const uint32_t leaf = blockIdx.x % kTreeLeaves;
+    const uint32_t n_leaf = (gridDim.x - leaf + kTreeLeaves - 1) / kTreeLeaves;
+    const uint32_t n_root = gridDim.x < (uint32_t)kTreeLeaves ? gridDim.x : (uint32_t)kTreeLeaves;
+    uint32_t* lc = tree + leaf * kTicketStride;
+    if (counter_add(lc) + 1u == n_leaf) {
+        counter_reset(lc);
+        uint32_t* rc = tree + kTreeLeaves * kTicketStride;
+        if (counter_add(rc) + 1u == n_root) {
+            counter_reset(rc);
+            __hip_atomic_store(gen, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    const uint64_t t0 = wall_clock64();
+    while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target) {
+        if (wall_clock64() - t0 > kSpinTicks) {
+            atomicOr(err, kErrSpinTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+}  // namespace moa

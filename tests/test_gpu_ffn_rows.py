@@ -1,0 +1,94 @@
+"""decoder_feedforward at 2..16 token rows: the matrix-core path (moa_rows.hip) that reads each
+weight once for all rows, in all three weight formats, vs the CPU oracle (which runs the
+reference's per-row algorithm, generate_references.py:375-414). Calls of more rows run in tiles of
+16 for the FP4 formats (a last tile of one row takes the single-row kernel). Each output row depends
+on its own input row only: the first rows of a call give the same bits as a call of just those
+rows."""
+import numpy as np
+import pytest
+
+from gpu_util import gate, gate_addend, need_gpu, say
+from moa_amd import synth
+from test_gpu_ffn import (FFN_ATOL, cancellation_residual, gpu_fp8, gpu_mxfp4, gpu_nvfp4, oracle_fp8, oracle_mxfp4,
+                          oracle_nvfp4)
+
+pytestmark = pytest.mark.gpu
+H = 3840
+FORMATS = {"fp8": (oracle_fp8, gpu_fp8), "nvfp4": (oracle_nvfp4, gpu_nvfp4), "mxfp4": (oracle_mxfp4, gpu_mxfp4)}
+_weights = {}
+
+
+def case(fmt: str, M: int, tag: str = "rows") -> dict:
+    """The format's weights (generated once) with M residual rows ~ N(0, 1)."""
+    if fmt not in _weights:
+        if fmt == "fp8":
+            _weights[fmt] = synth.cfg_ffn_fp8(7)
+        elif fmt == "mxfp4":
+            _weights[fmt] = synth.cfg_ffn_mxfp4(7)
+        else:
+            _weights[fmt] = synth.ref_ffn_inputs(1)  # the reference harness's NVFP4 weights and scales
+    d = dict(_weights[fmt])
+    d["residual"] = synth.bf16_normal(f"{tag}.{fmt}.residual", (M, H))
+    return d
+
+
+@pytest.mark.parametrize("M", [2, 5, 16])
+@pytest.mark.parametrize("fmt", ["fp8", "nvfp4", "mxfp4"])
+def test_rows_match_oracle(fmt, M):
+    need_gpu()
+    say(f"ffn rows {fmt} M{M}")
+    want, got = FORMATS[fmt]
+    d = case(fmt, M)
+    gate(want(d), got(d), f"ffn rows {fmt} M{M}", atol=FFN_ATOL)
+    from moa_amd import ops
+    assert ops.device_errors() == 0  # no grid-barrier wait of the single launch timed out
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "nvfp4", "mxfp4"])
+def test_rows_are_independent_and_repeatable(fmt):
+    need_gpu()
+    say(f"ffn rows {fmt}: M16 vs M3 prefix, repeat")
+    _, got = FORMATS[fmt]
+    d16 = case(fmt, 16, "indep")
+    d3 = dict(d16, residual=d16["residual"][:3].copy())
+    a = got(d16)
+    assert np.array_equal(a[:3], got(d3))
+    assert np.array_equal(a, got(d16))
+
+
+@pytest.mark.parametrize("fmt", ["nvfp4", "mxfp4"])
+def test_fp4_calls_of_17_rows_run_in_tiles(fmt):
+    need_gpu()
+    say(f"ffn rows {fmt} M17")
+    want, got = FORMATS[fmt]
+    d = case(fmt, 17, "tiles")
+    gate(want(d), got(d), f"ffn rows {fmt} M17", atol=FFN_ATOL)
+
+
+def test_rows_without_post_norm_and_layer_scalar():
+    need_gpu()
+    say("ffn rows fp8 M3 without post-norm and layer scalar")
+    d = case("fp8", 3, "plain")
+    gate_addend(oracle_fp8(d, False, False), gpu_fp8(d, False, False), d["residual"], "ffn rows fp8 M3 plain",
+                atol=FFN_ATOL)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+def test_rows_cancellation_probe(fmt):
+    """Rows whose pre-normed activations cancel in every up/gate row (the config-3 probe), mixed
+    with ordinary rows."""
+    need_gpu()
+    say(f"ffn rows {fmt} cancellation probe M4")
+    want, got = FORMATS[fmt]
+    d = case(fmt, 4, "cancel")
+    d["residual"] = d["residual"].copy()
+    d["residual"][1] = cancellation_residual(-23)
+    d["residual"][3] = cancellation_residual(-12)
+    d["pre_ff_rms_weight"] = np.full(H, 0x3F80, np.uint16)
+    if fmt == "fp8":
+        for k in ("up_weight", "gate_weight"):
+            w = d[k].copy()
+            w[:, 0::480] = 0x38  # 1.0
+            w[:, 1::480] = 0x38
+            d[k] = w
+    gate(want(d), got(d), f"ffn rows {fmt} cancel M4", atol=FFN_ATOL)
