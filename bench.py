@@ -49,6 +49,10 @@ MALL_BYTES = 256 << 20
 # Algorithmic bytes per call (weights + scales + operator-boundary vectors).
 FATTN_PAGES = 8  # full-attention decode at position 4095: pages 0..7
 BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
+         # config 3, MXFP4 weights (E2M1 codes + E8M0 block-32 scales) at M = 1 and M = 16 rows: the
+         # weights once, plus the rows' residual read and write, the two norm weights, the layer scalar
+         "ffn_mxfp4": 94_003_200 + 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
+         "ffn_mxfp4_m16": 94_003_200 + 16 * 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
          # sliding_attention, all 1024 slots valid: K and V caches + q + out + mask row
          "attn": 2 * 1024 * 8 * 256 * 2 + 2 * 4096 * 2 + 1024 * 4,
          # final_norm_and_logits: the bf16 lm_head (262144 x 3840) + input + norm weight + logits
@@ -84,6 +88,7 @@ def main() -> int:
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
+                                          "ffn_mxfp4", "ffn_mxfp4_m16",
                              "chunk"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
@@ -155,6 +160,14 @@ def main() -> int:
     fa_out = torch.zeros(8192, dtype=torch.int16, device="cuda")
     f_res, f_pre, f_post, f_ls = (dev(ffn[k]) for k in ("residual", "pre_ff_rms_weight", "post_ff_rms_weight",
                                                           "layer_scalar"))
+    # config 3: MXFP4 weights, one row and 16 rows
+    mx = synth.cfg_ffn_mxfp4(0, M=16)
+    MXK = ("up_weight_packed", "gate_weight_packed", "down_weight_packed", "up_weight_scale", "gate_weight_scale",
+           "down_weight_scale")
+    nmx = copies(BYTES["ffn_mxfp4"])
+    MXW = replicate(mx, MXK, nmx)
+    mx_res16 = dev(mx["residual"])
+    mx_res1 = mx_res16[:1].clone()
     o_x, o_post, o_res = dev(o["x"]), dev(o["post_attn_rms_weight"]), dev(o["residual"])
     q = {k: dev(qkv[k]) for k in ("x", "input_rms_weight", "q_rms_weight", "k_rms_weight", "cos", "sin",
                                   "k_cache", "v_cache")}
@@ -202,6 +215,13 @@ def main() -> int:
         ops.decoder_feedforward_fp8(f_res, f_pre, w["up_weight"], w["gate_weight"], w["down_weight"],
                                     w["up_weight_scale"], w["gate_weight_scale"], w["down_weight_scale"],
                                     f_post, f_ls)
+
+    def run_ffn_mxfp4(i, res=None):
+        w = MXW[i % nmx]
+        ops.decoder_feedforward_mxfp4(mx_res1 if res is None else res, f_pre, *[w[k] for k in MXK], f_post, f_ls)
+
+    def run_ffn_mxfp4_m16(i):
+        run_ffn_mxfp4(i, mx_res16)
 
     def run_o(i):
         w = OW[i % no]
@@ -288,8 +308,8 @@ def main() -> int:
     if args.profile:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
-              "fattn_fused64": run_fattn_fused64, "fo": run_fo,
-              "chunk": run_layer}[args.profile]
+              "fattn_fused64": run_fattn_fused64, "fo": run_fo, "ffn_mxfp4": run_ffn_mxfp4,
+              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -302,7 +322,8 @@ def main() -> int:
         return 0
 
     per_op = {}
-    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("attn", run_attn), ("logits", run_logits),
+    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
+                     ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("attn", run_attn), ("logits", run_logits),
                      ("fqkv", run_fqkv), ("fattn", run_fattn), ("fattn_fused", run_fattn_fused),
                      ("fattn_fused64", run_fattn_fused64), ("fo", run_fo)):
         ms, _ = graph_timed(fn, args.steps, args.warmup)

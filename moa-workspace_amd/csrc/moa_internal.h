@@ -37,10 +37,7 @@ constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
 constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN workgroups each
 // sliding_attention: one counter per (row, head) of a launch, 32 arrivals per launch, never reset
 constexpr int kTicketAttn = kTicketFfnEpoch + 16;
-// grid barrier of the single-launch FFN for 2..16 rows (moa_rows.hip): a 17-counter tree and a generation word
-constexpr int kTicketRowsBar = kTicketAttn + kMaxDecodeM * kNs;
-constexpr int kTicketRowsGen = kTicketRowsBar + kTreeCounters;
-constexpr int kTicketCount = kTicketRowsGen + 1;
+constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;
 // sliding_attention partials: [kMaxDecodeM][kNs][32 chunks][kGs][max, sum, o[kDs]]
 constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (4 + kDs);
 // full-attention page partials: per token row and 64-slot chunk, 16 maxima, 16 sums, out [16][512]
@@ -85,7 +82,6 @@ struct DevCtx {
     int8_t o_fused[2] = {-1, -1};                    // per scale kind
     int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
     int8_t full_o_fused[2] = {-1, -1};               // the same for full_attention_output
-    int8_t rows_fused[6] = {-1, -1, -1, -1, -1, -1}; // per (format, scale kind): single-launch rows FFN fits?
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
