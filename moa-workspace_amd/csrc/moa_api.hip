@@ -50,7 +50,6 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_err = carve(sizeof(uint32_t) * 4);
     const size_t t_raw = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * (kQs + 2 * kPs));
     const size_t t_p = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kL);
-    const size_t t_d = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_h = carve(sizeof(uint16_t) * (size_t)kMaxChunkM * kH);
     const size_t t_f = carve(sizeof(float) * kChunkPartFloats);
     const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
@@ -78,7 +77,6 @@ DevCtx* device_context(hipError_t* err) {
     c.err = reinterpret_cast<uint32_t*>(b + t_err);
     c.raw_qkv = reinterpret_cast<uint16_t*>(b + t_raw);
     c.pbuf = reinterpret_cast<uint16_t*>(b + t_p);
-    c.dbuf = reinterpret_cast<uint16_t*>(b + t_d);
     c.hbuf = reinterpret_cast<uint16_t*>(b + t_h);
     c.fbuf = reinterpret_cast<float*>(b + t_f);
     c.ffn_part = reinterpret_cast<uint64_t*>(b + t_part);

@@ -985,7 +985,6 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
 constexpr int kUgRL = 8;     // L rows (an up row and a gate row each) per wave
 constexpr int kUgDepth = 2;  // up/gate pipeline ring depth
 constexpr int kUgPre = 1;    // ring stages issued before the pre-norm completes (<= kUgDepth - 1)
-constexpr int kDownR = 2;    // down rows per wave (two-launch path)
 
 template <FfnFormat F>
 constexpr int row_bytes(int k) { return F == FfnFormat::FP8 ? k : k / 2; }
@@ -1097,25 +1096,6 @@ __device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t
     return pv;
 }
 
-// The wave's first n (<= R, uniform over the wave) down rows row0 .., every chunk's load issued
-// at once.
-template <FfnFormat F, int R>
-__device__ __forceinline__ void down_issue(Chunk<F> (&cb)[R][down_chunks<F>()], const FfnParams& p, int row0, int n,
-                                           int lane) {
-    constexpr int RB = row_bytes<F>(kL);
-    constexpr int SB = scale_row_bytes<F>(kL);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r < n) {
-#pragma unroll
-            for (int j = 0; j < down_chunks<F>(); ++j)
-                load_chunk<F>(cb[r][j], p.down + (size_t)(row0 + r) * RB,
-                              p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
-                              j * 1024 + lane * 16 < RB);
-        }
-    }
-}
-
 // Chunk j of each of the wave's first n (<= R, uniform over the wave) down rows row0 ...
 template <FfnFormat F, int R>
 __device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnParams& p, int row0, int n, int j,
@@ -1128,75 +1108,6 @@ __device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnPa
             load_chunk<F>(dst[r], p.down + (size_t)(row0 + r) * RB,
                           p.down_s ? (const uint8_t*)p.down_s + (size_t)(row0 + r) * SB : nullptr, j, lane,
                           j * 1024 + lane * 16 < RB);
-}
-
-// Dots of the wave's first n down rows with p (bf16 in LDS); lane r < n returns row r's.
-template <FfnFormat F, int R>
-__device__ __forceinline__ float down_dots(const Chunk<F> (&cb)[R][down_chunks<F>()], const uint16_t* __restrict__ pl,
-                                           int n, int lane) {
-    constexpr int EPC = elems_per_chunk<F>();
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < down_chunks<F>(); ++j) {
-        const int e0 = j * 64 * EPC + lane * EPC;
-        if (e0 < kL) {
-            uint32_t x[EPC / 2];
-            lds_pairs<EPC>(pl, e0, x);
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r < n) acc[r] = chunk_dot2<F>(x, cb[r][j], acc[r]);
-        }
-    }
-    float mine = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r < n) {
-            const float d = wave_sum(acc[r]);
-            if (lane == r) mine = d;
-        }
-    }
-    return mine;
-}
-
-// ------------------------------------------------------------ two launches (2..16 token rows)
-template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(kBlock) void ffn_up_gate_kernel(FfnParams p, int m0, uint16_t* pbuf_all) {
-    __shared__ uint16_t hs[kH];
-    __shared__ float red[4];
-    const int m = blockIdx.y;
-    const int lane = lane_id();
-    const int lbase = blockIdx.x * (4 * kUgRL) + wave_id();  // stage g: four consecutive rows
-    const float pv = up_gate_rows<F, SK, 4>(p, p.residual + (size_t)(m0 + m) * kH, lbase, 4, hs, red);
-    if (lane < kUgRL) pbuf_all[(size_t)m * kL + lbase + 4 * lane] = (uint16_t)f2bf(pv);
-}
-
-template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(kBlock) void ffn_down_kernel(FfnParams p, int m0, const uint16_t* pbuf_all,
-                                                          uint16_t* dbuf_all, uint32_t* tickets) {
-    __shared__ uint16_t ps[kL];
-    const int m = blockIdx.y;
-    const int lane = lane_id();
-    const int row0 = blockIdx.x * (4 * kDownR) + wave_id() * kDownR;
-
-    const float my_scale = row_scale<F, SK>(p.down_s, p.down_g, row0 + min(lane, kDownR - 1));
-    RowStage<kL / 8> st;
-    row_issue(st, pbuf_all + (size_t)m * kL);
-    Chunk<F> cb[kDownR][down_chunks<F>()];
-    down_issue<F, kDownR>(cb, p, row0, kDownR, lane);
-#pragma unroll
-    for (int i = 0; i < RowStage<kL / 8>::N; ++i) {
-        const int c = threadIdx.x + i * kBlock;
-        if (c < kL / 8) *reinterpret_cast<uint4*>(ps + c * 8) = st.v[i];
-    }
-    __syncthreads();
-    const float mine = down_dots<F, kDownR>(cb, ps, kDownR, lane);
-    uint16_t* dbuf = dbuf_all + (size_t)m * kH;
-    if (lane < kDownR) publish(&dbuf[row0 + lane], f2bf(proj_commit<F>(mine, my_scale)));
-
-    if (!block_arrive_tree(&tickets[(kTicketFfn + m * kTreeCounters) * kTicketStride], gridDim.x)) return;
-    block_post_residual(dbuf, p.post_rms, p.residual + (size_t)(m0 + m) * kH, p.layer_scalar);
 }
 
 // ------------------------------------------------------------ single launch (one token row)

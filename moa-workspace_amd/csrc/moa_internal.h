@@ -20,15 +20,14 @@ constexpr size_t kChunkPartFloats = (size_t)kMaxChunkM * kQkvRowsTotal;
 // Arrival counters. Each counter owns a 256-byte line: device-scope atomics to one line
 // serialise (~15 ns each), so counters never share a line and each kernel arrives once per
 // workgroup. Layout (in counters): [0, 32*kMaxDecodeM) QKV per (row, head);
-// then per row a 17-counter tree (16 leaves + 1 root) for O and again for the FFN down; then the
-// grid barrier of the single-launch FFN (a 17-counter tree and a generation word).
+// then per row a 17-counter tree (16 leaves + 1 root) for O; then the grid barrier of the
+// single-launch FFN (a 17-counter tree and a generation word).
 constexpr int kTicketStride = 64;  // uint32 per counter (256 bytes)
 constexpr int kTreeLeaves = 16;
 constexpr int kTreeCounters = kTreeLeaves + 1;
 constexpr int kTicketQkv = 0;
 constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
-constexpr int kTicketFfn = kTicketO + kTreeCounters * kMaxDecodeM;
-constexpr int kTicketFfnBar = kTicketFfn + kTreeCounters * kMaxDecodeM;
+constexpr int kTicketFfnBar = kTicketO + kTreeCounters * kMaxDecodeM;
 constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
 // Epoch counters of the single-launch O (16) and QKV (one per head) kernels: monotonic, never
 // reset; a workgroup adds one at entry and divides what it read by the workgroups per counter.
@@ -67,7 +66,6 @@ struct DevCtx {
     uint32_t* err = nullptr;      // 4 words
     uint16_t* raw_qkv = nullptr;  // [kMaxChunkM, 8192] bf16 raw projections
     uint16_t* pbuf = nullptr;     // [kMaxChunkM, 15360] bf16 (O: [M,3840]; FFN: GeGLU output)
-    uint16_t* dbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (FFN down output)
     uint16_t* hbuf = nullptr;     // [kMaxChunkM, 3840] bf16 (normalised activations, MFMA path)
     float* fbuf = nullptr;        // [splits][M][N] f32 split-K partial sums (MFMA path), kChunkPartFloats
     uint64_t* ffn_part = nullptr;  // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
