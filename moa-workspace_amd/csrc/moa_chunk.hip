@@ -611,6 +611,18 @@ hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, De
         : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
 }
 
+hipError_t launch_qkv_heads(const QkvParams& p, int m0, int M, const float* part, int splits, hipStream_t s, DevCtx* ctx) {
+    return p.scale_kind == ScaleKind::F32
+        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32>, dim3(32, M), s, p, m0, M, part, splits, ctx->err)
+        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16>, dim3(32, M), s, p, m0, M, part, splits, ctx->err);
+}
+
+hipError_t launch_post_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk, const uint16_t* w_post,
+                            uint16_t* res, const uint16_t* ls, hipStream_t s) {
+    return sk == ScaleKind::F32 ? post_rows<ScaleKind::F32>(part, splits, M, scale, w_post, res, ls, s)
+                                : post_rows<ScaleKind::BF16>(part, splits, M, scale, w_post, res, ls, s);
+}
+
 hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, hipStream_t s) {
     return ck_launch(chunk_rmsnorm_rows_kernel<false>, dim3(M), s, x, w, out);
 }

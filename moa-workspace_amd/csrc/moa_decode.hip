@@ -24,6 +24,9 @@ namespace moa {
 namespace {
 
 constexpr int kBlock = 256;  // four waves
+// Calls of at least this many rows (and at most kMaxDecodeM) run sliding QKV and O on the
+// matrix-core rows path (moa_rows.hip), which reads the weights once instead of once per row.
+constexpr int kRowsProjMinM = 3;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
@@ -1412,6 +1415,11 @@ hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* c
                 continue;
             }
         }
+        if (mm >= kRowsProjMinM) {  // the matrix-core rows path reads the weights once for all rows
+            const hipError_t e = launch_qkv_rows(p, m0, mm, s, ctx);
+            if (e != hipSuccess) return e;
+            continue;
+        }
         const dim3 grid(kQkvRows / (4 * kQkvR), mm);
         hipError_t e = p.scale_kind == ScaleKind::F32
             ? launch(qkv_decode_kernel<ScaleKind::F32, false>, grid, s, p, m0, ctx->raw_qkv, ctx->tickets, ctx->err)
@@ -1467,6 +1475,11 @@ static hipError_t o_decode_impl(const OParams& p, int M, hipStream_t s, DevCtx* 
                 if (e != hipSuccess) return e;
                 continue;
             }
+        }
+        if (KX == kQs && !p.div && mm >= kRowsProjMinM) {  // sliding O: the matrix-core rows path
+            const hipError_t e = launch_o_rows(p, m0, mm, s, ctx);
+            if (e != hipSuccess) return e;
+            continue;
         }
         const dim3 grid(kH / (4 * kOR), mm);
         hipError_t e = p.scale_kind == ScaleKind::F32

@@ -150,6 +150,14 @@ hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, Dev
 hipError_t launch_ffn_post_rows(const FfnParams& p, const float* part, int splits, int M, uint16_t* res, hipStream_t s);
 // out[m] = bf16(RMSNorm(x[m]) * w) for M rows of kH, row-major (gemma4.py:83-89).
 hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, hipStream_t s);
+// The row kernels after a split-K contraction of M rows (partials [splits][M][N] f32): the QKV heads
+// (scale, head RMSNorm, RoPE, q_out / ring-cache stores) and the O post (scale, post-RMSNorm, residual).
+hipError_t launch_qkv_heads(const QkvParams& p, int m0, int M, const float* part, int splits, hipStream_t s, DevCtx* ctx);
+hipError_t launch_post_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk, const uint16_t* w_post,
+                            uint16_t* res, const uint16_t* ls, hipStream_t s);
+// sliding_project_qkv / sliding_attention_output for 2..kMaxDecodeM rows on the matrix cores (moa_rows.hip).
+hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 
 // ops::final_norm_and_logits for M token rows (input [M][kH], out [M][kW]).
 hipError_t launch_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_w, const uint16_t* w, uint16_t* out,

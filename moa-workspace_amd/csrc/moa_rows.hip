@@ -31,8 +31,12 @@ typedef __bf16 rw_bf16x2 __attribute__((ext_vector_type(2)));
 constexpr int kRwTile = 16;                    // weight rows per wave (the MFMA's N)
 constexpr int kRwGroupRows = 4 * kRwTile;      // weight rows per workgroup
 constexpr int kRwK = 3840;                     // k per workgroup: all of H (up/gate), a quarter of L (down)
-constexpr int kRwRowUnits = kRwK / 8 + 1;      // 16-byte LDS units per activation row, one of them padding
-constexpr int kRwLdsUnits = (kMaxDecodeM * kRwRowUnits + 63) / 64 * 64;  // whole 1 KB blocks
+// 16-byte LDS units per activation row of k range KR, one of them padding (so that 16 rows start on
+// distinct LDS banks), and the LDS of 16 such rows
+template <int KR>
+constexpr int rw_row_units() { return KR / 8 + 1; }
+template <int KR>
+constexpr int rw_lds_units() { return (kMaxDecodeM * rw_row_units<KR>() + 63) / 64 * 64; }
 constexpr int kRwSplits = kL / kRwK;           // down: four k quarters
 constexpr int kRwUpGroups = kL / kRwGroupRows;      // 240 up/gate workgroups
 constexpr int kRwDownGroups = kH / kRwGroupRows;    // 60 down column groups (x 4 quarters)
@@ -41,7 +45,7 @@ constexpr int kRwCompute = 4 * kRwNH;
 static_assert(kH == kRwK && kL == kRwSplits * kRwK, "one workgroup k range");
 static_assert(kL % kRwGroupRows == 0 && kH % kRwGroupRows == 0, "whole weight tiles");
 static_assert(kRwDownGroups * kRwSplits == kRwUpGroups, "one grid for both contractions");
-static_assert((kRwRowUnits * 4) % 64 == 4, "row stride: 16 rows start on distinct LDS banks");
+static_assert((rw_row_units<kRwK>() * 4) % 64 == 4, "row stride: 16 rows start on distinct LDS banks");
 
 // k covered by one 16-byte weight load of each lane (FP8: 16 codes; FP4: 32 codes), and the
 // wave's load step (four lane groups side by side).
@@ -133,13 +137,13 @@ struct RwShape {
 };
 
 // One wave's weight stream: a 16-row tile (GeGLU: of up and of gate) over one part of the
-// workgroup's k range, the FP4 block-scale codes of that range, and the ring of loads.
-template <FfnFormat F, bool G>
+// workgroup's k range KR, the FP4 block-scale codes of that range, and the ring of loads.
+template <FfnFormat F, bool G, int KR = kRwK>
 struct RwStream {
     static constexpr int NM = G ? 2 : 1;
     static constexpr int NH = RwShape<F, G>::NH, D = RwShape<F, G>::D, B = RwShape<F, G>::B;
     static constexpr int LK = rw_lane_k<F>(), SKK = rw_step_k<F>();
-    static constexpr int KW = kRwK / NH;  // k per wave
+    static constexpr int KW = KR / NH;    // k per wave
     static constexpr int S = KW / SKK;    // load steps per wave
     static constexpr int EPB = F == FfnFormat::FP8 ? 1 : 2;                                    // elements per byte
     static constexpr int BLK = F == FfnFormat::MXFP4 ? 32 : (F == FfnFormat::NVFP4 ? 16 : 1);  // scale block
@@ -152,10 +156,10 @@ struct RwStream {
 
 // The stream of lane (r, g) for weight rows n0 .. n0 + 15 of w0 (and w1), k kb .. kb + KW of rows
 // of wk elements: the scale codes, then the first D - B load steps.
-template <FfnFormat F, bool G>
-__device__ __forceinline__ void rw_prefetch(RwStream<F, G>& st, const uint8_t* w0, const uint8_t* w1, const void* s0,
+template <FfnFormat F, bool G, int KR>
+__device__ __forceinline__ void rw_prefetch(RwStream<F, G, KR>& st, const uint8_t* w0, const uint8_t* w1, const void* s0,
                                             const void* s1, int wk, int n0, int kb, int r, int g) {
-    using T = RwStream<F, G>;
+    using T = RwStream<F, G, KR>;
 #pragma unroll
     for (int k = 0; k < T::NM; ++k) {
         st.wp[k] = (k ? w1 : w0) + (size_t)(n0 + r) * (wk / T::EPB) + kb / T::EPB + 16 * g;
@@ -183,31 +187,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rw_rsrc(const void* base, uint
 // and rows past M hold zeros. The loads go out first (rw_rows_load), the weight ring next, and the
 // LDS stores (rw_rows_store) then wait for these loads only -- loads complete in order, so the
 // ring stays in flight (a load straight into LDS would need a wait for every load).
-template <int NT>
+template <int NT, int KR = kRwK>
 struct RwRows {
-    static constexpr int N = (kMaxDecodeM * kRwRowUnits + NT - 1) / NT;
+    static constexpr int RU = rw_row_units<KR>();
+    static constexpr int N = (kMaxDecodeM * RU + NT - 1) / NT;
     uint4 v[N];
 };
 
-template <int NT>
-__device__ __forceinline__ void rw_rows_load(RwRows<NT>& st, const uint16_t* x, int ldx, int kz, int M, int t) {
+template <int NT, int KR>
+__device__ __forceinline__ void rw_rows_load(RwRows<NT, KR>& st, const uint16_t* x, int ldx, int kz, int M, int t) {
+    using R = RwRows<NT, KR>;
     const __amdgpu_buffer_rsrc_t rs = rw_rsrc(x, (uint32_t)(sizeof(uint16_t) * (size_t)M * ldx));
 #pragma unroll
-    for (int i = 0; i < RwRows<NT>::N; ++i) {
-        const int u = t + NT * i, m = u / kRwRowUnits, c = u % kRwRowUnits;
-        const bool ok = m < M && c < kRwK / 8;
+    for (int i = 0; i < R::N; ++i) {
+        const int u = t + NT * i, m = u / R::RU, c = u % R::RU;
+        const bool ok = m < M && c < KR / 8;
         const uint4 v = __builtin_bit_cast(
             uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (int)(sizeof(uint16_t) * (m * ldx + kz + c * 8)) : 0, 0, 0));
         st.v[i] = ok ? v : make_uint4(0, 0, 0, 0);
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void rw_rows_store(const RwRows<NT>& st, uint4* xs, int t) {
+template <int NT, int KR>
+__device__ __forceinline__ void rw_rows_store(const RwRows<NT, KR>& st, uint4* xs, int t) {
+    using R = RwRows<NT, KR>;
 #pragma unroll
-    for (int i = 0; i < RwRows<NT>::N; ++i) {
+    for (int i = 0; i < R::N; ++i) {
         const int u = t + NT * i;
-        if (u < kMaxDecodeM * kRwRowUnits) xs[u] = st.v[i];
+        if (u < kMaxDecodeM * R::RU) xs[u] = st.v[i];
     }
     rw_lds_barrier<-1>();
 }
@@ -217,14 +224,14 @@ __device__ __forceinline__ void rw_rows_store(const RwRows<NT>& st, uint4* xs, i
 // each step runs its MFMAs. MFMA j of a step takes the lane's k 8 j .. 8 j + 7 of its load -- for
 // A (LDS row r) and B alike, a fixed permutation of the step's k. acc[k][e]: row 4 g + e, weight
 // row r of the tile.
-template <FfnFormat F, bool G>
-__device__ __forceinline__ void rw_mma(RwStream<F, G>& st, const uint4* xs, f32x4 (&acc)[G ? 2 : 1], int part, int r,
+template <FfnFormat F, bool G, int KR>
+__device__ __forceinline__ void rw_mma(RwStream<F, G, KR>& st, const uint4* xs, f32x4 (&acc)[G ? 2 : 1], int part, int r,
                                        int g) {
-    using T = RwStream<F, G>;
+    using T = RwStream<F, G, KR>;
     constexpr int D = T::D, B = T::B, S = T::S;
 #pragma unroll
     for (int k = 0; k < T::NM; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int abase = r * kRwRowUnits + (part * T::KW + g * T::LK) / 8;
+    const int abase = r * rw_row_units<KR>() + (part * T::KW + g * T::LK) / 8;
     const uint32_t gsh = F == FfnFormat::MXFP4 ? 8 * g : 16 * (g & 1);  // this lane group's code(s) in sd
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -317,7 +324,7 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
                                                                           uint16_t* y, float* yf) {
     using T = RwStream<F, G>;
     constexpr int NW = 4 * T::NH;
-    __shared__ __attribute__((aligned(16))) uint4 xs[kRwLdsUnits];
+    __shared__ __attribute__((aligned(16))) uint4 xs[rw_lds_units<kRwK>()];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int tile = wave & 3, part = wave >> 2;
     const int r = lane & 15, g = lane >> 4;
@@ -326,11 +333,11 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
     RwRows<64 * NW> rows;
     rw_rows_load<64 * NW>(rows, x, ldx, kz, M, t);
     T st;
-    if constexpr (G) rw_prefetch<F, G>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, kz + part * T::KW, r, g);
-    else rw_prefetch<F, G>(st, p.down, nullptr, p.down_s, nullptr, kL, n0, kz + part * T::KW, r, g);
+    if constexpr (G) rw_prefetch<F, G, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, kz + part * T::KW, r, g);
+    else rw_prefetch<F, G, kRwK>(st, p.down, nullptr, p.down_s, nullptr, kL, n0, kz + part * T::KW, r, g);
     rw_rows_store(rows, xs, t);
     f32x4 acc[T::NM];
-    rw_mma<F, G>(st, xs, acc, part, r, g);
+    rw_mma<F, G, kRwK>(st, xs, acc, part, r, g);
     rw_reduce<T::NM, T::NH>(acc, xs, tile, part, lane);
     if (part != 0) return;
     if constexpr (G) rw_geglu_out<F, SK>(acc, p, y, n0 + r, M, g);
@@ -355,7 +362,87 @@ hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCt
     return launch_ffn_post_rows(p, ctx->fbuf, kRwSplits, M, p.residual + (size_t)m0 * kH, s);
 }
 
+// ---------------------------------------------------------------- FP8 projections (QKV, O)
+// Y[M][N] = X[M][K] . W[N][K]^T as split-K f32 partial sums [gridDim.z][M][N]; column n of the
+// output uses weight matrix w[i] (its row n - nseg[i]); a workgroup's 64 columns never straddle two
+// matrices. The scales are applied by the row kernels that sum the partials.
+struct ProjRows {
+    const uint16_t* x;  // [M][K] bf16 rows
+    int M, K, N;
+    const uint8_t* w[3];
+    int nseg[4];
+    int nsegs;
+    float* yf;
+};
+
+template <int KR>
+__global__ __launch_bounds__((256 * kRwNH)) void rows_proj_kernel(ProjRows a) {
+    using T = RwStream<FfnFormat::FP8, false, KR>;
+    constexpr int NW = 4 * T::NH;
+    __shared__ __attribute__((aligned(16))) uint4 xs[rw_lds_units<KR>()];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int tile = wave & 3, part = wave >> 2;
+    const int r = lane & 15, g = lane >> 4;
+    const int c0 = blockIdx.x * kRwGroupRows;
+    int seg = 0;
+    while (seg + 1 < a.nsegs && c0 >= a.nseg[seg + 1]) ++seg;
+    const int n0 = c0 - a.nseg[seg] + tile * kRwTile;  // row of w[seg]
+    const int kz = blockIdx.z * KR;
+    RwRows<64 * NW, KR> rows;
+    rw_rows_load<64 * NW>(rows, a.x, a.K, kz, a.M, t);
+    T st;
+    rw_prefetch<FfnFormat::FP8, false, KR>(st, a.w[seg], nullptr, nullptr, nullptr, a.K, n0, kz + part * T::KW, r, g);
+    rw_rows_store(rows, xs, t);
+    f32x4 acc[1];
+    rw_mma<FfnFormat::FP8, false, KR>(st, xs, acc, part, r, g);
+    rw_reduce<1, T::NH>(acc, xs, tile, part, lane);
+    if (part != 0) return;
+    const int n = c0 + tile * kRwTile + r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = 4 * g + e;
+        if (m < a.M) a.yf[((size_t)blockIdx.z * a.M + m) * a.N + n] = acc[0][e];
+    }
+}
+
+template <int KR>
+hipError_t rw_proj(const ProjRows& a, hipStream_t s) {
+    if (a.N % kRwGroupRows || a.K % KR) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((rows_proj_kernel<KR>), dim3(a.N / kRwGroupRows, 1, a.K / KR), dim3(256 * kRwNH), 0, s, a);
+    return hipGetLastError();
+}
+
+constexpr int kRwQkvKR = 1920;  // QKV: 128 column groups x 2 halves of H
+constexpr int kRwOKR = 1024;    // O: 60 column groups x 4 quarters of the 4096 inputs
+static_assert((rw_row_units<kRwQkvKR>() * 4) % 64 == 4 && (rw_row_units<kRwOKR>() * 4) % 64 == 4, "LDS banks");
+
 }  // namespace
+
+hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
+    hipError_t e = launch_rmsnorm_rows(p.x + (size_t)m0 * kH, p.in_rms, ctx->hbuf, M, s);
+    if (e != hipSuccess) return e;
+    ProjRows a{};
+    a.x = ctx->hbuf; a.M = M; a.K = kH; a.N = kQkvRowsTotal;
+    a.w[0] = p.qw; a.w[1] = p.kw; a.w[2] = p.vw;
+    a.nseg[0] = 0; a.nseg[1] = kQs; a.nseg[2] = kQs + kPs; a.nseg[3] = kQkvRowsTotal; a.nsegs = 3;
+    a.yf = ctx->fbuf;
+    e = rw_proj<kRwQkvKR>(a, s);
+    if (e != hipSuccess) return e;
+    return launch_qkv_heads(p, m0, M, ctx->fbuf, kH / kRwQkvKR, s, ctx);
+}
+
+hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    if (M < 1 || M > kMaxDecodeM || p.div) return hipErrorInvalidValue;
+    ProjRows a{};
+    a.x = p.x + (size_t)m0 * kQs; a.M = M; a.K = kQs; a.N = kH;
+    a.w[0] = p.ow; a.nseg[0] = 0; a.nseg[1] = kH; a.nsegs = 1;
+    a.yf = ctx->fbuf;
+    const hipError_t e = rw_proj<kRwOKR>(a, s);
+    if (e != hipSuccess) return e;
+    return launch_post_rows(ctx->fbuf, kQs / kRwOKR, M, p.os, p.scale_kind, p.post_rms, p.residual + (size_t)m0 * kH,
+                            nullptr, s);
+}
 
 hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
     if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
