@@ -389,8 +389,8 @@ __global__ __launch_bounds__(kCkBlock) void chunk_tile_rows_kernel(const uint16_
 // Per (head, row): raw = bf16((sum of the split-K partials) * s), RMSNorm over the head's 256 raw
 // values (q, k weighted; v plain), RoPE on q and k, and the q_out / ring-cache stores
 // (generate_references.py:265-274; sliding/rmsnorm.rs:22-153, rope.rs:9-211, ops.rs:72-75).
-// Thread t owns head element t; RoPE partners (t, t ^ 128) meet in LDS. A bad offset writes
-// nothing; workgroup (0, 0) reports it.
+// Thread t owns head element t; RoPE partners (t, t ^ 128) meet in LDS. A row whose offsets are bad
+// writes nothing, and its head-0 workgroup reports them.
 template <ScaleKind SK>
 __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, int m0, int M,
                                                                    const float* __restrict__ part, int splits,
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
     const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + mm < kE;
     const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
     if (!rope_ok || !kv_ok) {
-        if (head == 0 && m == 0 && t == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
+        if (head == 0 && t == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
         return;
     }
     const int slot = (kv_off / (kNs * kDs * 2) + mm) % kTs;

@@ -1433,6 +1433,11 @@ hipError_t launch_full_qkv(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx
     static_assert(kFqkvRows <= kL, "raw full-layer projections fit a pbuf row");
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
+        if (mm >= kRowsProjMinM) {  // the matrix-core rows path
+            const hipError_t e = launch_full_qkv_rows(p, m0, mm, s, ctx);
+            if (e != hipSuccess) return e;
+            continue;
+        }
         const dim3 grid(kFqkvRows / (4 * kQkvR), mm);
         // raw projections in pbuf, rows kFqkvRows apart (pbuf holds kMaxChunkM x kL >= 16 x 8704)
         hipError_t e = p.scale_kind == ScaleKind::F32
@@ -1476,7 +1481,8 @@ static hipError_t o_decode_impl(const OParams& p, int M, hipStream_t s, DevCtx* 
                 continue;
             }
         }
-        if (KX == kQs && !p.div && mm >= kRowsProjMinM) {  // sliding O: the matrix-core rows path
+        // the matrix-core rows path (full-attention O, K = 8192: from two rows on)
+        if (mm >= (KX == kQf ? 2 : kRowsProjMinM)) {
             const hipError_t e = launch_o_rows(p, m0, mm, s, ctx);
             if (e != hipSuccess) return e;
             continue;

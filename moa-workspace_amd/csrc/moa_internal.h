@@ -155,9 +155,11 @@ hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* o
 hipError_t launch_qkv_heads(const QkvParams& p, int m0, int M, const float* part, int splits, hipStream_t s, DevCtx* ctx);
 hipError_t launch_post_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk, const uint16_t* w_post,
                             uint16_t* res, const uint16_t* ls, hipStream_t s);
-// sliding_project_qkv / sliding_attention_output for 2..kMaxDecodeM rows on the matrix cores (moa_rows.hip).
+// sliding_project_qkv and sliding / full attention output for 2..kMaxDecodeM rows on the matrix cores
+// (moa_rows.hip).
 hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
+hipError_t launch_full_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 
 // ops::final_norm_and_logits for M token rows (input [M][kH], out [M][kW]).
 hipError_t launch_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_w, const uint16_t* w, uint16_t* out,

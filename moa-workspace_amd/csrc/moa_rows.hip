@@ -194,8 +194,12 @@ struct RwRows {
     uint4 v[N];
 };
 
+// With div (full-attention output: the running softmax sums [M][16] of the 512-element heads), each
+// element becomes bf16(x / sum), or zero where the sum is not positive -- as the per-row kernels'
+// o_input_chunk.
 template <int NT, int KR>
-__device__ __forceinline__ void rw_rows_load(RwRows<NT, KR>& st, const uint16_t* x, int ldx, int kz, int M, int t) {
+__device__ __forceinline__ void rw_rows_load(RwRows<NT, KR>& st, const uint16_t* x, int ldx, int kz, int M, int t,
+                                             const float* div = nullptr) {
     using R = RwRows<NT, KR>;
     const __amdgpu_buffer_rsrc_t rs = rw_rsrc(x, (uint32_t)(sizeof(uint16_t) * (size_t)M * ldx));
 #pragma unroll
@@ -205,6 +209,22 @@ __device__ __forceinline__ void rw_rows_load(RwRows<NT, KR>& st, const uint16_t*
         const uint4 v = __builtin_bit_cast(
             uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (int)(sizeof(uint16_t) * (m * ldx + kz + c * 8)) : 0, 0, 0));
         st.v[i] = ok ? v : make_uint4(0, 0, 0, 0);
+    }
+    if (div) {
+#pragma unroll
+        for (int i = 0; i < R::N; ++i) {
+            const int u = t + NT * i, m = u / R::RU, c = u % R::RU;
+            if (m < M && c < KR / 8) {
+                const float d = div[m * kGf + (kz + c * 8) / kDf];
+                float f[8];
+                bf16x8_to_f32(st.v[i], f);
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    h[e] = f2bf(d > 0.0f ? f[2 * e] / d : 0.0f) | (f2bf(d > 0.0f ? f[2 * e + 1] / d : 0.0f) << 16);
+                st.v[i] = make_uint4(h[0], h[1], h[2], h[3]);
+            }
+        }
     }
 }
 
@@ -368,6 +388,7 @@ hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCt
 // matrices. The scales are applied by the row kernels that sum the partials.
 struct ProjRows {
     const uint16_t* x;  // [M][K] bf16 rows
+    const float* div;   // full-attention output: running sums [M][16] dividing x (or null)
     int M, K, N;
     const uint8_t* w[3];
     int nseg[4];
@@ -389,7 +410,7 @@ __global__ __launch_bounds__((256 * kRwNH)) void rows_proj_kernel(ProjRows a) {
     const int n0 = c0 - a.nseg[seg] + tile * kRwTile;  // row of w[seg]
     const int kz = blockIdx.z * KR;
     RwRows<64 * NW, KR> rows;
-    rw_rows_load<64 * NW>(rows, a.x, a.K, kz, a.M, t);
+    rw_rows_load<64 * NW>(rows, a.x, a.K, kz, a.M, t, a.div);
     T st;
     rw_prefetch<FfnFormat::FP8, false, KR>(st, a.w[seg], nullptr, nullptr, nullptr, a.K, n0, kz + part * T::KW, r, g);
     rw_rows_store(rows, xs, t);
@@ -414,9 +435,93 @@ hipError_t rw_proj(const ProjRows& a, hipStream_t s) {
 
 constexpr int kRwQkvKR = 1920;  // QKV: 128 column groups x 2 halves of H
 constexpr int kRwOKR = 1024;    // O: 60 column groups x 4 quarters of the 4096 inputs
-static_assert((rw_row_units<kRwQkvKR>() * 4) % 64 == 4 && (rw_row_units<kRwOKR>() * 4) % 64 == 4, "LDS banks");
+constexpr int kRwFoKR = 2048;   // full-attention O: 60 column groups x 4 quarters of the 8192 inputs
+static_assert((rw_row_units<kRwQkvKR>() * 4) % 64 == 4 && (rw_row_units<kRwOKR>() * 4) % 64 == 4 &&
+                  (rw_row_units<kRwFoKR>() * 4) % 64 == 4, "LDS banks");
+
+// Block sum over the workgroup's NW waves, in wave order.
+template <int NW>
+__device__ __forceinline__ float rw_block_sum(float v, float* red, int lane, int wave) {
+    v = wave_sum(v);
+    if (lane == 0) red[wave] = v;
+    rw_lds_barrier<-1>();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += red[w];
+    rw_lds_barrier<-1>();
+    return tot;
+}
+
+// full_project_qkv heads after the split-K contraction: workgroup (head, row), head < 16 a query
+// head, head 16 the one KV head; thread t owns elements t and t + 256 of the head's 512. raw =
+// bf16(sum of the partials * scale), then as the per-row kernels' head epilogue (full/rmsnorm.rs,
+// rope.rs; generate_references.py:265-274): RMSNorm over the head (weighted for q and k; V is the
+// unweighted norm of the same raw K), RoPE (the table's sin has its low half negated: plain half
+// swap), q_out / page-slot stores. A row whose offsets are bad writes nothing, and its head-0
+// workgroup reports them.
+template <ScaleKind SK>
+__global__ __launch_bounds__(256) void rows_fqkv_heads_kernel(QkvParams p, int m0, int M, const float* __restrict__ part,
+                                                              int splits, uint32_t* err) {
+    constexpr int Hf = kDf / 2, N = kQf + kPf;
+    __shared__ float red[4];
+    const int head = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+    const int mm = m0 + m;
+    const int32_t rope_off = *p.rope_off, kv_off = *p.kv_off;
+    const bool rope_ok = rope_off >= 0 && (rope_off % (kDf * 2)) == 0 && rope_off / (kDf * 2) + mm < kE;
+    const bool kv_ok = kv_off >= 0 && (kv_off % (kDf * 2)) == 0 && kv_off / (kDf * 2) + mm < kTf;
+    if (!rope_ok || !kv_ok) {
+        if (head == 0 && t == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
+        return;
+    }
+    const int slot = kv_off / (kDf * 2) + mm;
+    const int trow = rope_off / (kDf * 2) + mm;
+    float raw[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int col = head * kDf + t + h * Hf;
+        float a = 0.0f;
+        for (int z = 0; z < splits; ++z) a = z == 0 ? part[((size_t)z * M + m) * N + col] : a + part[((size_t)z * M + m) * N + col];
+        const float sc = head < kGf ? rw_row_scale<SK>(p.qs, col) : rw_row_scale<SK>(p.ks, col - kQf);
+        raw[h] = rbf(a * sc);
+    }
+    const uint16_t* wn = head < kGf ? p.q_rms : p.k_rms;
+    const float w0 = bf2f(wn[t]), w1 = bf2f(wn[t + Hf]);
+    const float c0 = bf2f(p.cos[(size_t)trow * kDf + t]), c1 = bf2f(p.cos[(size_t)trow * kDf + t + Hf]);
+    const float s0 = bf2f(p.sin[(size_t)trow * kDf + t]), s1 = bf2f(p.sin[(size_t)trow * kDf + t + Hf]);
+    const float inv = rms_inverse(rw_block_sum<4>(raw[0] * raw[0] + raw[1] * raw[1], red, t & 63, t >> 6), kDf);
+    const float u0 = raw[0] * inv, u1 = raw[1] * inv;
+    if (head == kGf) {  // V: the unweighted norm
+        p.v_cache[(size_t)slot * kDf + t] = (uint16_t)f2bf(u0);
+        p.v_cache[(size_t)slot * kDf + t + Hf] = (uint16_t)f2bf(u1);
+    }
+    const float n0 = rbf(u0 * w0), n1 = rbf(u1 * w1);
+    uint16_t* dst = head < kGf ? p.q_out + (size_t)mm * kQf + head * kDf : p.k_cache + (size_t)slot * kDf;
+    dst[t] = (uint16_t)f2bf(rbf(n0 * c0) + rbf(n1 * s0));
+    dst[t + Hf] = (uint16_t)f2bf(rbf(n1 * c1) + rbf(n0 * s1));
+}
 
 }  // namespace
+
+hipError_t launch_full_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
+    hipError_t e = launch_rmsnorm_rows(p.x + (size_t)m0 * kH, p.in_rms, ctx->hbuf, M, s);
+    if (e != hipSuccess) return e;
+    ProjRows a{};
+    a.x = ctx->hbuf; a.M = M; a.K = kH; a.N = kQf + kPf;
+    a.w[0] = p.qw; a.w[1] = p.kw;
+    a.nseg[0] = 0; a.nseg[1] = kQf; a.nseg[2] = kQf + kPf; a.nsegs = 2;
+    a.yf = ctx->fbuf;
+    e = rw_proj<kRwQkvKR>(a, s);
+    if (e != hipSuccess) return e;
+    const int sp = kH / kRwQkvKR;
+    if (p.scale_kind == ScaleKind::F32)
+        hipLaunchKernelGGL((rows_fqkv_heads_kernel<ScaleKind::F32>), dim3(kGf + 1, M), dim3(256), 0, s, p, m0, M,
+                           (const float*)ctx->fbuf, sp, ctx->err);
+    else
+        hipLaunchKernelGGL((rows_fqkv_heads_kernel<ScaleKind::BF16>), dim3(kGf + 1, M), dim3(256), 0, s, p, m0, M,
+                           (const float*)ctx->fbuf, sp, ctx->err);
+    return hipGetLastError();
+}
 
 hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
     if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
@@ -433,15 +538,17 @@ hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, Dev
 }
 
 hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
-    if (M < 1 || M > kMaxDecodeM || p.div) return hipErrorInvalidValue;
+    if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
+    const bool full = p.div != nullptr;  // full-attention layer: 8192 inputs divided by the running sums
+    const int K = full ? kQf : kQs;
     ProjRows a{};
-    a.x = p.x + (size_t)m0 * kQs; a.M = M; a.K = kQs; a.N = kH;
+    a.x = p.x + (size_t)m0 * K; a.div = full ? p.div + (size_t)m0 * kGf : nullptr; a.M = M; a.K = K; a.N = kH;
     a.w[0] = p.ow; a.nseg[0] = 0; a.nseg[1] = kH; a.nsegs = 1;
     a.yf = ctx->fbuf;
-    const hipError_t e = rw_proj<kRwOKR>(a, s);
+    const hipError_t e = full ? rw_proj<kRwFoKR>(a, s) : rw_proj<kRwOKR>(a, s);
     if (e != hipSuccess) return e;
-    return launch_post_rows(ctx->fbuf, kQs / kRwOKR, M, p.os, p.scale_kind, p.post_rms, p.residual + (size_t)m0 * kH,
-                            nullptr, s);
+    return launch_post_rows(ctx->fbuf, K / (full ? kRwFoKR : kRwOKR), M, p.os, p.scale_kind, p.post_rms,
+                            p.residual + (size_t)m0 * kH, nullptr, s);
 }
 
 hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {

@@ -58,3 +58,38 @@ def test_o_rows_are_independent():
     d16 = synth.cfg_o(12, M=16)
     d4 = dict(d16, x=d16["x"][:4].copy(), residual=d16["residual"][:4].copy())
     assert np.array_equal(o_gpu(d16)[:4], o_gpu(d4))
+
+
+@pytest.mark.parametrize("pos", [16, 3000])
+def test_full_qkv_rows_match_oracle(pos):
+    """full_project_qkv at 16 rows (17 heads of 512 from [Wq; Wk]; V the unweighted norm of K)."""
+    need_gpu()
+    from moa_amd import ops
+    from test_gpu_full import TF, qkv_gpu as fq_gpu, qkv_oracle as fq_oracle
+    say(f"full qkv rows M16 pos={pos}")
+    d = synth.cfg_full_qkv(seed=13, M=16, pos=pos)
+    gq, gk, gv = fq_gpu(d, 16)
+    assert ops.device_errors() == 0
+    wq, wk, wv = fq_oracle(d, 16)
+    gate(wq, gq, f"full q_out rows pos{pos}")
+    gate(wk, gk, f"full k page rows pos{pos}")
+    gate(wv, gv, f"full v page rows pos{pos}")
+    slot = pos % TF
+    keep = np.ones(TF, bool)
+    keep[slot:slot + 16] = False
+    assert np.array_equal(gk[keep], d["k_cache"][keep]) and np.array_equal(gv[keep], d["v_cache"][keep])
+
+
+@pytest.mark.parametrize("M", [2, 16])
+def test_full_output_rows_match_oracle(M):
+    """full_attention_output at 2 and 16 rows: x divided by the running sums (a head without a
+    valid slot gives zeros), K = 8192."""
+    need_gpu()
+    from test_gpu_full import out_gpu as fo_gpu, out_oracle as fo_oracle
+    say(f"full output rows M{M}")
+    d = synth.cfg_full_o(seed=14, M=M)
+    d["running_sum"][1, 7] = 0.0
+    d["running_sum"][M - 1, 0] = 0.0
+    a = fo_gpu(d)
+    gate(fo_oracle(d), a, f"full output rows M{M}")
+    assert np.array_equal(a, fo_gpu(d))
