@@ -41,7 +41,6 @@ constexpr int kRwSplits = kL / kRwK;           // down: four k quarters
 constexpr int kRwUpGroups = kL / kRwGroupRows;      // 240 up/gate workgroups
 constexpr int kRwDownGroups = kH / kRwGroupRows;    // 60 down column groups (x 4 quarters)
 constexpr int kRwNH = 2;                       // k parts per workgroup: 8 compute waves
-constexpr int kRwCompute = 4 * kRwNH;
 static_assert(kH == kRwK && kL == kRwSplits * kRwK, "one workgroup k range");
 static_assert(kL % kRwGroupRows == 0 && kH % kRwGroupRows == 0, "whole weight tiles");
 static_assert(kRwDownGroups * kRwSplits == kRwUpGroups, "one grid for both contractions");
