@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kCkBlock) void chunk_tile_rows_kernel(const uint16_
 // (generate_references.py:265-274; sliding/rmsnorm.rs:22-153, rope.rs:9-211, ops.rs:72-75).
 // Thread t owns head element t; RoPE partners (t, t ^ 128) meet in LDS. A row whose offsets are bad
 // writes nothing, and its head-0 workgroup reports them.
-template <ScaleKind SK>
+template <ScaleKind SK, int ZS = kCkSplitMax>
 __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, int m0, int M,
                                                                    const float* __restrict__ part, int splits,
                                                                    uint32_t* err) {
@@ -409,12 +409,12 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
     const int slot = (kv_off / (kNs * kDs * 2) + mm) % kTs;
     const int trow = rope_off / (kDs * 2) + mm;
     const int col = head * kDs + t;
-    float pz[kCkSplitMax];  // all partial loads in flight at once (index clamped), summed in split order
+    float pz[ZS];  // all partial loads in flight at once (index clamped), summed in split order
 #pragma unroll
-    for (int z = 0; z < kCkSplitMax; ++z) pz[z] = part[((size_t)min(z, splits - 1) * M + m) * kQkvRowsTotal + col];
+    for (int z = 0; z < ZS; ++z) pz[z] = part[((size_t)min(z, splits - 1) * M + m) * kQkvRowsTotal + col];
     float acc = pz[0];
 #pragma unroll
-    for (int z = 1; z < kCkSplitMax; ++z) acc = z < splits ? acc + pz[z] : acc;
+    for (int z = 1; z < ZS; ++z) acc = z < splits ? acc + pz[z] : acc;
     const float sc = head < 16 ? chunk_scale<SK>(p.qs, col)
                                : (head < 24 ? chunk_scale<SK>(p.ks, col - kQs) : chunk_scale<SK>(p.vs, col - kQs - kPs));
     const float v = rbf(acc * sc);
@@ -444,7 +444,8 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
 // Per row: d = bf16((sum of the split-K partials) * s[n]), then out = bf16(bf16(r + N(d)) * ls)
 // with N the post-RMSNorm (identity when w_post is null) and ls skipped when null
 // (shared/rmsnorm.rs:204-296, residual.rs:189-241; generate_references.py:411-413).
-template <ScaleKind SK, FfnFormat F = FfnFormat::FP8>
+// ZS: the most splits a call may have (the loads of all of them are in flight at once).
+template <ScaleKind SK, FfnFormat F = FfnFormat::FP8, int ZS = kCkSplitMax>
 __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* __restrict__ part, int splits, int M,
                                                                    const void* scale, const float* __restrict__ gscale,
                                                                    const uint16_t* __restrict__ w_post,
@@ -468,16 +469,16 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
         const int c = min(t + 256 * i, NC - 1);
         const bool act = t + 256 * i < NC;
         // all partial loads in flight at once (index clamped), then summed in split order
-        float4 u[kCkSplitMax], v[kCkSplitMax];
+        float4 u[ZS], v[ZS];
 #pragma unroll
-        for (int z = 0; z < kCkSplitMax; ++z) {
+        for (int z = 0; z < ZS; ++z) {
             const float* src = part + ((size_t)min(z, splits - 1) * M + m) * kH + c * 8;
             u[z] = *reinterpret_cast<const float4*>(src);
             v[z] = *reinterpret_cast<const float4*>(src + 4);
         }
         float a[8] = {u[0].x, u[0].y, u[0].z, u[0].w, v[0].x, v[0].y, v[0].z, v[0].w};
 #pragma unroll
-        for (int z = 1; z < kCkSplitMax; ++z) {
+        for (int z = 1; z < ZS; ++z) {
             const bool on = z < splits;
             a[0] = on ? a[0] + u[z].x : a[0]; a[1] = on ? a[1] + u[z].y : a[1];
             a[2] = on ? a[2] + u[z].z : a[2]; a[3] = on ? a[3] + u[z].w : a[3];
@@ -551,6 +552,9 @@ int m_tiles(int M) { return (M + kCkBM - 1) / kCkBM; }
 template <ScaleKind SK>
 hipError_t post_rows(const float* part, int splits, int M, const void* scale, const uint16_t* w_post, uint16_t* res,
                      const uint16_t* ls, hipStream_t s) {
+    if (splits <= 4)
+        return ck_launch(chunk_post_rows_kernel<SK, FfnFormat::FP8, 4>, dim3(M), s, part, splits, M, scale,
+                         (const float*)nullptr, w_post, res, ls);
     return ck_launch(chunk_post_rows_kernel<SK>, dim3(M), s, part, splits, M, scale, (const float*)nullptr, w_post, res, ls);
 }
 
@@ -612,9 +616,10 @@ hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, De
 }
 
 hipError_t launch_qkv_heads(const QkvParams& p, int m0, int M, const float* part, int splits, hipStream_t s, DevCtx* ctx) {
+    if (splits > 2) return hipErrorInvalidValue;
     return p.scale_kind == ScaleKind::F32
-        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32>, dim3(32, M), s, p, m0, M, part, splits, ctx->err)
-        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16>, dim3(32, M), s, p, m0, M, part, splits, ctx->err);
+        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32, 2>, dim3(32, M), s, p, m0, M, part, splits, ctx->err)
+        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16, 2>, dim3(32, M), s, p, m0, M, part, splits, ctx->err);
 }
 
 hipError_t launch_post_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk, const uint16_t* w_post,
@@ -633,10 +638,12 @@ hipError_t launch_ffn_post_rows(const FfnParams& p, const float* part, int split
             return p.scale_kind == ScaleKind::F32 ? post_rows<ScaleKind::F32>(part, splits, M, p.down_s, p.post_rms, res, p.layer_scalar, s)
                                                   : post_rows<ScaleKind::BF16>(part, splits, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
         case FfnFormat::NVFP4:
-            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::NVFP4>, dim3(M), s, part, splits, M,
+            if (splits > 4) return hipErrorInvalidValue;
+            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::NVFP4, 4>, dim3(M), s, part, splits, M,
                              (const void*)nullptr, p.down_g, p.post_rms, res, p.layer_scalar);
         case FfnFormat::MXFP4:
-            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::MXFP4>, dim3(M), s, part, splits, M,
+            if (splits > 4) return hipErrorInvalidValue;
+            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::MXFP4, 4>, dim3(M), s, part, splits, M,
                              (const void*)nullptr, (const float*)nullptr, p.post_rms, res, p.layer_scalar);
     }
     return hipErrorInvalidValue;
