@@ -986,7 +986,8 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
 // device at once; otherwise, and for 2..16 rows (grid.y = row), they are two launches.
 // Activations (normalised x, p) are bf16 in LDS and enter the dot products as bf16 pairs.
 constexpr int kUgRL = 8;     // L rows (an up row and a gate row each) per wave
-constexpr int kUgDepth = 2;  // up/gate pipeline ring depth
+constexpr int kUgDepth = 2;  // up/gate pipeline ring depth (FP8 rows)
+constexpr int kUgDepthFp4 = 2;  // the same for FP4 rows, half as long (measured: depths 3 and 4 are slower)
 constexpr int kUgPre = 1;    // ring stages issued before the pre-norm completes (<= kUgDepth - 1)
 
 template <FfnFormat F>
@@ -1036,7 +1037,7 @@ __device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t
     constexpr int SB = scale_row_bytes<F>(kH);
     constexpr int KI = (RB + 1023) / 1024;
     constexpr int RL = kUgRL;
-    constexpr int D = kUgDepth;
+    constexpr int D = F == FfnFormat::FP8 ? kUgDepth : kUgDepthFp4;
     const int lane = lane_id();
 
     Chunk<F> ring[D][2][KI];
