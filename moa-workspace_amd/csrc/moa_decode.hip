@@ -983,7 +983,7 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
 //   up_gate: pre-RMSNorm, up and gate rows, GeGLU -> p[15360] (bf16)
 //   down:    p . W_down rows -> d[3840], then post-norm, residual and the layer scalar in place.
 // One token row runs both halves in a single launch (ffn_fused_kernel) when its grid fits on the
-// device at once; otherwise, and for 2..16 rows (grid.y = row), they are two launches.
+// device at once; otherwise, and for 2..16 rows, the matrix-core rows path (moa_rows.hip) runs them.
 // Activations (normalised x, p) are bf16 in LDS and enter the dot products as bf16 pairs.
 constexpr int kUgRL = 8;     // L rows (an up row and a gate row each) per wave
 constexpr int kUgDepth = 2;  // up/gate pipeline ring depth (FP8 rows)
@@ -1124,20 +1124,15 @@ __device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnPa
 // Two grid-wide dependencies: every down row needs all 15360 GeGLU values (p), and the post-norm
 // of every output needs the sum of squares of all 3840 down outputs.
 //
-// p, FP8 weights: tagged words instead of a barrier. Every workgroup's control wave publishes the
-// workgroup's 64 GeGLU values as 32 64-bit words (two bf16 values and the launch's tag). It issues
-// them before any other load of the workgroup: a CU serves its loads in order, so the words are
-// not queued behind the workgroup's weight loads. Then every thread issues its first read of p
-// (15 words; workgroups start at different words so that they do not all request one line), and
-// every wave issues its first kFfnDownPre down chunks. Words that do not yet carry the tag are read
-// again until they do. No atomic arrival or poll sits between the last workgroup's up/gate rows and
-// everyone's p.
-// p, FP4 weights: a barrier. The control wave publishes, then arrives on a 16-leaf arrival tree
-// plus a generation word that moves by one per launch: the control wave reads it at entry (g0);
-// the workgroup that completes the tree resets the tree and stores g0 + 1; the others poll until
-// it reads g0 + 1, then stage p into LDS. Waves 0-6 issue their first kFfnDownPre down chunks
-// before the barrier. The control wave issues its own only after staging p, since a wave with
-// weight loads in flight would see the barrier only once they had landed.
+// p: tagged words instead of a barrier. Every workgroup's control wave publishes the workgroup's
+// 64 GeGLU values as 32 64-bit words (two bf16 values and the launch's tag). It issues them before
+// any other load of the workgroup: a CU serves its loads in order, so the words are not queued
+// behind the workgroup's weight loads. Then every thread issues its first read of p (15 words;
+// workgroups start at different words so that they do not all request one line), and every wave
+// issues its first kFfnDownPre down chunks. Words that do not yet carry the tag are read again
+// until they do. No atomic arrival or poll sits between the last workgroup's up/gate rows and
+// everyone's p. (FP4 weights used an arrival-tree barrier here before; the tagged words measured
+// 0.2-0.35 us faster.)
 // The launch's tag is ep + 1: 16 counters, each advanced by 15 workgroups per launch of any format,
 // give ep. Tags therefore never repeat across launches, so a word left by an earlier launch never
 // carries the current tag.
@@ -1169,8 +1164,7 @@ __device__ __forceinline__ void reload_stale(uint64_t (&w)[N], uint32_t tag, A a
 
 template <FfnFormat F, ScaleKind SK>
 __global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostSlots* slots, uint32_t* tickets,
-                      uint32_t* err) {
+void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uint32_t* tickets, uint32_t* err) {
     constexpr int KD = down_chunks<F>();
     constexpr int EPC = elems_per_chunk<F>();
     __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
@@ -1181,9 +1175,6 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostS
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
     const bool leader = blockIdx.x < kPostLeaders;
-    uint32_t* gen = tickets + kTicketFfnGen * kTicketStride;
-    uint32_t g0 = 0;
-    if (ctl) g0 = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // The launch's tag: 16 counters of 15 workgroups each advance by one per launch (every format
     // shares them, so post-norm slot tags never repeat across formats). Needed only after up/gate.
     uint32_t ep = 0;
@@ -1224,7 +1215,7 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostS
     constexpr int PD = kFfnDownPre < KD ? kFfnDownPre : KD;
     constexpr int RS = PD < KD ? PD + 1 : KD;  // ring slots
     Chunk<F> ring[RS][kFfnDownR];
-    if constexpr (F == FfnFormat::FP8) {
+    {
         // p by tagged words instead of a barrier. The control wave's 32 words (two GeGLU values and
         // the launch's tag each) are issued before any other load of the workgroup: a CU serves
         // its loads in order, so they are not queued behind this workgroup's weight loads. Every
@@ -1260,31 +1251,10 @@ void ffn_fused_kernel(FfnParams p, int m0, uint16_t* pbuf, uint64_t* ptag, PostS
         }
 #pragma unroll
         for (int i = 0; i < PW; ++i) *reinterpret_cast<uint32_t*>(sh + 2 * pword(i)) = (uint32_t)pw[i];
-    } else if (!ctl) {
-#pragma unroll
-        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
-    } else {
-        if (lane < kFfnWaves * kUgRL / 2)
-            publish32(pbuf + blockIdx.x * (kFfnWaves * kUgRL) + 2 * lane,
-                      f2bf(pl[2 * lane]) | (f2bf(pl[2 * lane + 1]) << 16));
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // published before arriving
-        if (lane == 0) grid_barrier(tickets + kTicketFfnBar * kTicketStride, gen, g0 + 1u, err);
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // no load below moves above the poll
-        // p into LDS straight from memory (no registers): 1920 chunks of 8, lane l moving chunks
-        // l + 64 i; agent-scope loads (sc1), like collect().
-#pragma unroll
-        for (int i = 0; i < kL / 8 / 64; ++i)
-            __builtin_amdgcn_global_load_lds((glb_void*)(pbuf + (lane + 64 * i) * 8), (lds_void*)(sh + 64 * 8 * i),
-                                             16, 0, 16 /* sc1 */);
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();  // p staged
 
     // ---- down: the ring streams the rest of the rows while the dots run
-    if (F != FfnFormat::FP8 && ctl) {  // issued after the barrier so that no other wave waits on these issues
-#pragma unroll
-        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
-    }
     {
         float acc[kFfnDownR];
 #pragma unroll
@@ -1524,7 +1494,7 @@ static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevC
         hipError_t e;
         if (mm == 1 && ffn_fused_fits<F, SK>(ctx)) {
             ffn_fused_kernel<F, SK><<<dim3(kFfnGrid), dim3(kFfnBlock), 0, s>>>(
-                p, m0, ctx->pbuf, ctx->ffn_ptag, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
+                p, m0, ctx->ffn_ptag, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
             continue;

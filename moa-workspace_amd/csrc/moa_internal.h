@@ -20,18 +20,15 @@ constexpr size_t kChunkPartFloats = (size_t)kMaxChunkM * kQkvRowsTotal;
 // Arrival counters. Each counter owns a 256-byte line: device-scope atomics to one line
 // serialise (~15 ns each), so counters never share a line and each kernel arrives once per
 // workgroup. Layout (in counters): [0, 32*kMaxDecodeM) QKV per (row, head);
-// then per row a 17-counter tree (16 leaves + 1 root) for O; then the grid barrier of the
-// single-launch FFN (a 17-counter tree and a generation word).
+// then per row a 17-counter tree (16 leaves + 1 root) for O.
 constexpr int kTicketStride = 64;  // uint32 per counter (256 bytes)
 constexpr int kTreeLeaves = 16;
 constexpr int kTreeCounters = kTreeLeaves + 1;
 constexpr int kTicketQkv = 0;
 constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
-constexpr int kTicketFfnBar = kTicketO + kTreeCounters * kMaxDecodeM;
-constexpr int kTicketFfnGen = kTicketFfnBar + kTreeCounters;
 // Epoch counters of the single-launch O (16) and QKV (one per head) kernels: monotonic, never
 // reset; a workgroup adds one at entry and divides what it read by the workgroups per counter.
-constexpr int kTicketOEpoch = kTicketFfnGen + 1;
+constexpr int kTicketOEpoch = kTicketO + kTreeCounters * kMaxDecodeM;
 constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
 constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN workgroups each
 // sliding_attention: one counter per (row, head) of a launch, 32 arrivals per launch, never reset

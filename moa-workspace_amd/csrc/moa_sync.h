@@ -63,29 +63,4 @@ __device__ __forceinline__ uint64_t collect64(const uint64_t* p) {
 }
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, uint32_t v) { return ((uint64_t)tag << 32) | v; }
 
-// One lane per workgroup, after its workgroup's results are published and complete: arrive on
-// `tree` (kTreeCounters counters kTicketStride apart) and wait until `gen` reads `target`.
-__device__ __forceinline__ void grid_barrier(uint32_t* tree, uint32_t* gen, uint32_t target, uint32_t* err) {
-    const uint32_t leaf = blockIdx.x % kTreeLeaves;
-    const uint32_t n_leaf = (gridDim.x - leaf + kTreeLeaves - 1) / kTreeLeaves;
-    const uint32_t n_root = gridDim.x < (uint32_t)kTreeLeaves ? gridDim.x : (uint32_t)kTreeLeaves;
-    uint32_t* lc = tree + leaf * kTicketStride;
-    if (counter_add(lc) + 1u == n_leaf) {
-        counter_reset(lc);
-        uint32_t* rc = tree + kTreeLeaves * kTicketStride;
-        if (counter_add(rc) + 1u == n_root) {
-            counter_reset(rc);
-            __hip_atomic_store(gen, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    const uint64_t t0 = wall_clock64();
-    while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target) {
-        if (wall_clock64() - t0 > kSpinTicks) {
-            atomicOr(err, kErrSpinTimeout);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-}
-
 }  // namespace moa
