@@ -1151,7 +1151,8 @@ constexpr int kFfnGrid = kL / (kFfnWaves * kUgRL);  // 240 workgroups
 constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgroup
 constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
 constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
-constexpr int kFfnDownPre = 4;                      // down chunks per row loaded before p is staged
+constexpr int kFfnDownPre = 4;                      // down chunks per row loaded before p is staged (FP8)
+constexpr int kFfnDownPreFp4 = 4;                   // the same for FP4 rows (8 chunks; measured: 2 equal, 6 and 8 slower)
 constexpr int kFfnEpochCounters = 16;               // launch-epoch counters (15 workgroups each)
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
 static_assert(kFfnGrid == kPostGrid && kFfnWgRows == kPostWgRows, "post-norm hand-off shape");
@@ -1212,7 +1213,8 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
 
     // Down loads only once the whole workgroup is through its up/gate rows (issued earlier they
     // would queue ahead of the slower waves' up/gate loads, which the barrier waits for).
-    constexpr int PD = kFfnDownPre < KD ? kFfnDownPre : KD;
+    constexpr int PDW = F == FfnFormat::FP8 ? kFfnDownPre : kFfnDownPreFp4;
+    constexpr int PD = PDW < KD ? PDW : KD;
     constexpr int RS = PD < KD ? PD + 1 : KD;  // ring slots
     Chunk<F> ring[RS][kFfnDownR];
     {
