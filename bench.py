@@ -10,10 +10,17 @@ MALL: all three weight sets fit the 256 MB Infinity Cache, so each operator cycl
 enough distinct weight copies (>= 512 MiB per operator) that no timed call re-reads cached
 weights.
 
-Timing: the K timed steps are replays of a HIP graph holding 40 consecutive steps (as a decode
-loop replays its captured layer), preceded by W warm-up steps; HIP events on the replay stream
-(the stream the kernels run on) bracket the replays, with synchronisations on both sides.
+Timing: the K timed steps (--steps) are captured once in a HIP graph (as a decode loop replays
+its captured layer); after W warm-up steps (--warmup, run as replays of the same graph) the graph
+is replayed R >= 20 times back to back, with a HIP event on the replay stream (the stream the
+kernels run on) between consecutive replays and synchronisations before the first and after the
+last. Each replay is one run of exactly K steps; `value` is the median over the R replays of the
+time per step, with p10 / p90 beside it. The operators are timed the same way (graphs of 40 calls).
 Host-driven times (one Python/ctypes call per launch) are reported beside them.
+
+Floor: an empty launch and a pure read of each operator's weight bytes (rotated past the MALL) at
+the operator's launch shape, with the library's stream-read kernel, and the attainable read rate
+of the device (1 GiB reads); the roofline's frac is also given against that attainable rate.
 
 The per-operator list also times sliding_attention (the step between QKV and O, outside the
 headline metric): one token over a full ring (1024 slots), caches rotated like the weights.
@@ -68,9 +75,14 @@ BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          # the same at the cache's full 64 pages (position 32767)
          "fattn_fused64": 64 * (2 * 512 * 512 * 2 + 512 * 4) + 8192 * 2 * 2 + 16 * 4 * 2}
 GRAPH_CALLS = 40  # calls per captured graph
+REPLAYS = 20  # timed replays per graph (median, p10, p90 over them)
 # Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
 FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+MFMA_FP8_PEAK_TFLOPS = 5000.0  # MI355X dense fp8
+# Launch shapes (workgroups, threads) of the one-token kernels, for the floor measurements.
+SHAPES = {"ffn": (240, 512), "o": (240, 512), "qkv": (256, 576)}
+WEIGHT_BYTES = {"ffn": 3 * 15360 * 3840, "o": 3840 * 4096, "qkv": 8192 * 3840}
 
 
 def log(*a):
@@ -283,27 +295,30 @@ def main() -> int:
         torch.cuda.synchronize()
         return a.elapsed_time(b) / steps  # ms per call
 
-    def graph_timed(fn, steps, warmup):
-        """Graph-driven: GRAPH_CALLS consecutive calls (cycling the weight copies) captured once in
-        a HIP graph and replayed; the events bracket whole replays on the replay stream."""
+    def graph_stats(fn, calls=GRAPH_CALLS, warmup=GRAPH_CALLS, replays=REPLAYS):
+        """Graph-driven: `calls` consecutive calls (cycling the weight copies) captured once in a
+        HIP graph; warm-up replays covering `warmup` calls, then `replays` replays back to back with
+        an event between consecutive ones on the replay stream. Returns the median, p10 and p90 of
+        ms per call over the replays."""
         for i in range(3):
             fn(i)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for i in range(GRAPH_CALLS):
+            for i in range(calls):
                 fn(i)
-        reps = max(1, math.ceil(steps / GRAPH_CALLS))
-        for _ in range(max(1, math.ceil(warmup / GRAPH_CALLS))):
+        for _ in range(max(1, math.ceil(warmup / calls))):
             g.replay()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+        ev[0].record()
+        for r in range(replays):
             g.replay()
-        b.record()
+            ev[r + 1].record()
         torch.cuda.synchronize()
-        return a.elapsed_time(b) / (reps * GRAPH_CALLS), reps * GRAPH_CALLS
+        per = np.array([ev[r].elapsed_time(ev[r + 1]) / calls for r in range(replays)])
+        del g
+        return float(np.median(per)), float(np.percentile(per, 10)), float(np.percentile(per, 90))
 
     if args.profile:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
@@ -321,35 +336,42 @@ def main() -> int:
         assert ops.device_errors() == 0
         return 0
 
+    floor = floor_measure(torch, np)
+
     per_op = {}
     for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
                      ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("attn", run_attn), ("logits", run_logits),
                      ("fqkv", run_fqkv), ("fattn", run_fattn), ("fattn_fused", run_fattn_fused),
                      ("fattn_fused64", run_fattn_fused64), ("fo", run_fo)):
-        ms, _ = graph_timed(fn, args.steps, args.warmup)
+        ms, p10, p90 = graph_stats(fn, replays=5 if name == "logits" else REPLAYS)
         ms_host = timed(fn, min(args.steps, 50), 5)
         gbps = BYTES[name] / (ms * 1e-3) / 1e9
-        per_op[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+        per_op[name] = {"us": round(ms * 1e3, 3), "us_p10": round(p10 * 1e3, 3), "us_p90": round(p90 * 1e3, 3),
+                        "GBps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                        "frac_attainable": round(gbps / floor["attainable_read_GBps"], 4),
                         "bytes": BYTES[name], "us_host_driven": round(ms_host * 1e3, 3)}
-        log(f"{name:13} {ms * 1e3:9.2f} us  {gbps:8.1f} GB/s  {100 * gbps / HBM_PEAK_GBPS:5.1f}% of 8 TB/s"
-            f"   (host-driven {ms_host * 1e3:.2f} us)")
+        log(f"{name:13} {ms * 1e3:9.2f} us [p10 {p10 * 1e3:.2f}, p90 {p90 * 1e3:.2f}]  {gbps:8.1f} GB/s  "
+            f"{100 * gbps / HBM_PEAK_GBPS:5.1f}% of 8 TB/s   (host-driven {ms_host * 1e3:.2f} us)")
 
-    ms_step, steps_done = graph_timed(run_step, args.steps, args.warmup)
+    # the headline: a graph of exactly K steps, replayed REPLAYS times after the warm-up
+    ms_step, step_p10, step_p90 = graph_stats(run_step, calls=args.steps, warmup=max(args.warmup, 1))
     ms_step_host = timed(run_step, min(args.steps, 50), 5)
-    log(f"step {ms_step * 1e3:9.2f} us/token   (host-driven {ms_step_host * 1e3:.2f} us)")
+    log(f"step {ms_step * 1e3:9.2f} us/token [p10 {step_p10 * 1e3:.2f}, p90 {step_p90 * 1e3:.2f}]   "
+        f"(host-driven {ms_step_host * 1e3:.2f} us)")
 
     chunk = None
     if CM:
-        chunk = {"rows": CM, "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "ops": {}}
+        chunk = {"rows": CM, "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "peak_fp8_TFLOPs": MFMA_FP8_PEAK_TFLOPS, "ops": {}}
         for name, fn in (("qkv", run_cqkv), ("o", run_co), ("ffn", run_cffn), ("layer", run_layer)):
-            ms, _ = graph_timed(fn, GRAPH_CALLS, GRAPH_CALLS)
+            ms, p10, p90 = graph_stats(fn, calls=8, warmup=8, replays=10)
             flops = CM * (sum(FLOPS_PER_ROW.values()) if name == "layer" else FLOPS_PER_ROW[name])
             tf = flops / (ms * 1e-3) / 1e12
-            chunk["ops"][name] = {"us": round(ms * 1e3, 2), "us_per_token": round(ms * 1e3 / CM, 4),
-                                  "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                                  "flops": flops}
+            chunk["ops"][name] = {"us": round(ms * 1e3, 2), "us_p10": round(p10 * 1e3, 2), "us_p90": round(p90 * 1e3, 2),
+                                  "us_per_token": round(ms * 1e3 / CM, 4), "TFLOPs": round(tf, 1),
+                                  "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                  "frac_fp8_peak": round(tf / MFMA_FP8_PEAK_TFLOPS, 4), "flops": flops}
             log(f"chunk M={CM} {name:5} {ms * 1e3:9.2f} us  {tf:7.1f} TFLOP/s  "
-                f"{100 * tf / MFMA_BF16_PEAK_TFLOPS:5.1f}% of bf16 MFMA peak")
+                f"{100 * tf / MFMA_BF16_PEAK_TFLOPS:5.1f}% of bf16 / {100 * tf / MFMA_FP8_PEAK_TFLOPS:5.1f}% of fp8 peak")
 
     ckpt = ckpt_measure(args.ckpt_gib) if args.ckpt_gib > 0 else None
     if ckpt:
@@ -380,7 +402,10 @@ def main() -> int:
         traffic = json.loads(tpath.read_text()).get("ffn_fused_kernel", {}).get("traffic_bytes")
     line = {
         "metric": METRIC, "value": round(ms_step * 1e3, 3), "unit": "us/token", "n_gpus": 1,
-        "steps": steps_done, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "timing": {"steps_per_replay": args.steps, "replays": REPLAYS, "steps_timed_total": args.steps * REPLAYS,
+                   "value_is": "median over replays of us per step", "us_p10": round(step_p10 * 1e3, 3),
+                   "us_p90": round(step_p90 * 1e3, 3)},
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8e4m3 weights x bf16 activations, f32 accumulate", "data": "synthetic",
         "config": {"workload": "decode step, M=1: sliding_project_qkv (cfg2) + sliding_attention_output (cfg1) "
@@ -388,9 +413,11 @@ def main() -> int:
                    "hidden": 3840, "intermediate": 15360, "tokens_per_step": 1},
         "roofline": {"bound": "hbm", "kernel": "decoder_feedforward_fp8 (ffn_fused_kernel, one launch)",
                      "achieved": f["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": f["frac"],
+                     "attainable": floor["attainable_read_GBps"], "frac_attainable": f["frac_attainable"],
                      "algorithmic_bytes": BYTES["ffn"], "avg_us": f["us"], "traffic": traffic,
                      "traffic_source": "profiles/hbm_traffic_m1.md" if traffic else None},
         "ops": per_op,
+        "floor": floor,
         "us_per_token_host_driven": round(ms_step_host * 1e3, 3),
         "hbm_copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": cpu,
@@ -454,6 +481,62 @@ def ckpt_measure(gib: float = 1.0):
     return {"GBps": round(gbps, 1), "pinned_copy_GBps": round(link, 1), "bytes": nbytes}
 
 
+def floor_measure(torch, np):
+    """The library's stream-read kernel (moa_bench_stream_read): the device's attainable read rate
+    (1 GiB per launch, best of three launch shapes), and per one-token operator an empty launch and
+    a pure read of its weight bytes at its launch shape, the windows rotated over 1 GiB so no
+    launch reads from the MALL. Graph-replayed like the operators."""
+    import ctypes as C
+
+    from moa_amd import _lib
+
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def read(nbytes, shape, rotate=True):
+        span = buf.numel() - nbytes
+        def fn(i):
+            off = ((i * nbytes) % span) // 256 * 256 if rotate and nbytes else 0
+            _lib.call("moa_bench_stream_read", C.c_void_p(buf.data_ptr() + off), C.c_uint64(nbytes), shape[0],
+                      shape[1], C.c_void_p(sink.data_ptr()), stream())
+        return fn
+
+    def stats(fn, calls=GRAPH_CALLS):
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(calls):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(REPLAYS + 1)]
+        ev[0].record()
+        for r in range(REPLAYS):
+            g.replay()
+            ev[r + 1].record()
+        torch.cuda.synchronize()
+        per = np.array([ev[r].elapsed_time(ev[r + 1]) / calls for r in range(REPLAYS)])
+        return float(np.median(per)) * 1e3  # us
+
+    out = {"attainable_shapes": {}}
+    for shape in ((1024, 512), (512, 1024), (2048, 256)):
+        us = stats(read(buf.numel(), shape, rotate=False), calls=8)
+        out["attainable_shapes"][f"{shape[0]}x{shape[1]}"] = round(buf.numel() / (us * 1e-6) / 1e9, 1)
+    out["attainable_read_GBps"] = max(out["attainable_shapes"].values())
+    for name, shape in SHAPES.items():
+        empty = stats(read(0, shape))
+        full = stats(read(WEIGHT_BYTES[name], shape))
+        out[name] = {"shape": list(shape), "empty_us": round(empty, 3), "read_us": round(full, 3),
+                     "read_bytes": WEIGHT_BYTES[name], "read_GBps": round(WEIGHT_BYTES[name] / (full * 1e-6) / 1e9, 1)}
+        log(f"floor {name:4} {shape}: empty launch {empty:.2f} us, read of {WEIGHT_BYTES[name]} B {full:.2f} us")
+    log(f"attainable read rate {out['attainable_read_GBps']:.1f} GB/s ({out['attainable_shapes']})")
+    del buf
+    return out
+
+
 LOGITS_CPU_ROWS = 16384  # vocabulary rows of the CPU logits sample (1/16 of the vocabulary)
 
 
@@ -502,7 +585,8 @@ def cpu_baseline(ffn, o, qkv, seconds: float):
 
     from oracle import oracle as O
 
-    cores = min(16, os.cpu_count() or 1)
+    avail = len(os.sched_getaffinity(0))
+    cores = min(avail, int(os.environ.get("OMP_NUM_THREADS") or avail))  # the box's CPU share
     O.set_threads(cores)
     w = O.ffn_weights(O.FFN_FP8, ffn["up_weight"], ffn["gate_weight"], ffn["down_weight"], ffn["up_weight_scale"],
                       ffn["gate_weight_scale"], ffn["down_weight_scale"])
@@ -517,17 +601,34 @@ def cpu_baseline(ffn, o, qkv, seconds: float):
         O.sliding_attention_output(o["x"], o["post_attn_rms_weight"], o["o_weight"], o["o_weight_scale"], r_o)
         O.decoder_feedforward(r_f, ffn["pre_ff_rms_weight"], w, ffn["post_ff_rms_weight"], ffn["layer_scalar"])
 
-    step()  # warm-up
-    times = []
-    t_end = time.time() + seconds
-    while time.time() < t_end or len(times) < 3:
-        t = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t)
-    us = float(np.median(times)) * 1e6
-    log(f"cpu oracle {us:9.1f} us/token on {cores} threads ({len(times)} steps)")
+    def median_us(n_min, budget):
+        step()  # warm-up
+        times = []
+        t_end = time.time() + budget
+        while time.time() < t_end or len(times) < n_min:
+            t = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t)
+        return float(np.median(times)) * 1e6, len(times)
+
+    us, n = median_us(20, seconds)
+    O.set_threads(1)
+    us1, n1 = median_us(20, 0.0)
+    O.set_threads(cores)
+    model = "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    log(f"cpu oracle {us:9.1f} us/token on {cores} threads ({n} steps), {us1:.1f} us on 1 thread ({n1} steps); "
+        f"{avail} cores available, {model}")
     return {"value": round(us, 1), "unit": "us/token", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} decode steps (M=1, cfg0+cfg1+cfg2), median; OpenMP {cores} threads"}
+            "cores_available": avail, "cpu_model": model, "one_thread_value": round(us1, 1),
+            "sample": f"{n} decode steps (M=1, cfg0+cfg1+cfg2), median, OpenMP {cores} threads; "
+                      f"1 thread: median of {n1} steps"}
 
 
 if __name__ == "__main__":

@@ -18,8 +18,9 @@
  *
  * Return value: MOA_SUCCESS or a negative MOA_ERROR_* code; moa_last_error_string() gives
  * the reason. Invalid arguments are rejected before anything is launched. Device-resident
- * offsets are validated by the kernel: an out-of-range offset writes nothing and raises a
- * bit read back by moa_device_errors().
+ * offsets are validated by the kernel: a token row whose RoPE row or ring slot is out of range
+ * writes nothing (the call's other rows are written) and raises a bit read back by
+ * moa_device_errors().
  *
  * Shapes (FO/src/axes.rs:3-29): H=3840 hidden, L=15360 intermediate, 8 KV heads x 2 query
  * heads x 256 head_dim (Q=4096, K/V=2048), ring cache T=1024 slots, RoPE table E=32768 rows.
@@ -42,8 +43,12 @@ extern "C" {
 
 #define MOA_DEVERR_ROPE_OFFSET 1u /* rope_offset not a multiple of 512 or past the table */
 #define MOA_DEVERR_KV_OFFSET 2u   /* kv_offset not a multiple of 4096 or past the ring */
-#define MOA_DEVERR_SPIN_TIMEOUT 4u /* a bounded cross-workgroup wait of a one-token call expired (the
-                                      call's results are unreliable; another process held the CUs) */
+#define MOA_DEVERR_SPIN_TIMEOUT 4u /* a bounded cross-workgroup wait of a one-token call expired
+                                      (another process held the CUs). The workgroups whose wait
+                                      expired store nothing: with the post-norm, the residual rows
+                                      behind an expired leader keep their input values, but rows of
+                                      other leaders may hold the result, so restore the outputs
+                                      from a copy before calling again. */
 
 /* Library version string. */
 const char* moa_version(void);
@@ -203,6 +208,21 @@ int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* 
  * final-logit softcap input with the kernels' own device helpers into out (device uint32
  * [132100]; layout in moa_decode.hip). */
 int moa_format_selftest(uint32_t* out, void* stream);
+
+/* Test support for the launch epochs of the one-token kernels (no counterpart in the reference).
+ * The one-token QKV (kernel 0), O (1) and FFN (2) kernels tag their cross-workgroup hand-off
+ * words with a per-launch tag derived from 64-bit epoch counters that `per` workgroups of each
+ * launch advance by one. moa_test_epoch_layout gives the number of counters and `per`;
+ * moa_test_epoch_tag computes, on the host, the tag a workgroup derives from the value `old` its
+ * add returned (the same function the kernels run). Neither touches a device. */
+int moa_test_epoch_layout(int kernel, int* counters, int* per);
+int moa_test_epoch_tag(int kernel, uint64_t old, uint32_t* tag);
+
+/* Test support: sets every epoch counter of the current device as if `launches` launches of each
+ * one-token kernel had run (counter = launches * per), and the sliding-attention tickets to
+ * (launches * 32) mod 2^32, so that a test can cross counter wrap points without running
+ * billions of launches. Synchronous; no call may be in flight on the device. */
+int moa_test_preset_epochs(uint64_t launches);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libmoa_gfx950.so"
-SOURCES = ["moa_api.hip", "moa_decode.hip", "moa_chunk.hip", "moa_attention.hip", "moa_logits.hip", "moa_ckpt.hip", "moa_full_attention.hip", "moa_rows.hip"]
+SOURCES = ["moa_api.hip", "moa_decode.hip", "moa_chunk.hip", "moa_attention.hip", "moa_logits.hip", "moa_ckpt.hip", "moa_full_attention.hip", "moa_rows.hip", "moa_bench.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -32,10 +32,7 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> Path:
-    srcs = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, "-o", str(tmp), *srcs]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -45,6 +42,25 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{msgs}")
     if verbose and msgs.strip():
         print(msgs)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compiles every source to an object (in parallel: the translation units are independent),
+    then links the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    objs = [objdir / (s.stem + ".o") for s in srcs]
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as ex:
+        for f in [ex.submit(_run, [HIPCC, *compile_flags, "-c", "-o", str(o), str(s)], verbose)
+                  for s, o in zip(srcs, objs)]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

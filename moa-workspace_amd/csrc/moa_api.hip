@@ -9,6 +9,7 @@
 
 #include "../../include/moa_ops.h"
 #include "moa_internal.h"
+#include "moa_sync.h"
 
 namespace moa {
 namespace {
@@ -170,7 +171,7 @@ int o_common(const OParams& p, int M, void* stream) {
     return MOA_SUCCESS;
 }
 
-int ffn_common(const FfnParams& p, int M, void* stream) {
+int ffn_check(const FfnParams& p, int M) {
     Check c;
     c.ptr(p.residual, "residual").ptr(p.pre_rms, "pre_ff_rms_weight");
     c.ptr(p.up, "up_weight").ptr(p.gate, "gate_weight").ptr(p.down, "down_weight");
@@ -188,7 +189,11 @@ int ffn_common(const FfnParams& p, int M, void* stream) {
         c.opt(p.post_rms, "post_ff_rms_weight").opt(p.layer_scalar, "layer_scalar", 2);
     }
     c.rows(M);
-    if (c.code) return c.code;
+    return c.code;
+}
+
+int ffn_common(const FfnParams& p, int M, void* stream) {
+    if (const int bad = ffn_check(p, M)) return bad;
     int code = MOA_SUCCESS;
     DevCtx* ctx = ctx_or_fail(&code);
     if (!ctx) return code;
@@ -418,6 +423,44 @@ int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* 
     if (M > 65535) return fail(MOA_ERROR_INVALID_VALUE, "M must be <= 65535 for the projection");
     ProjParams p{x, w, scale, ScaleKind::F32, out, N, K};
     return finish(launch_proj_decode(p, M, static_cast<hipStream_t>(stream)), "fp8_scaled_projection launch");
+}
+
+int moa_test_epoch_layout(int kernel, int* counters, int* per) {
+    if (!counters || !per) return fail(MOA_ERROR_INVALID_VALUE, "counters and per must not be NULL");
+    switch (kernel) {
+        case 0: *counters = kQkvEpochCounters; *per = kQkvEpochPer; return MOA_SUCCESS;
+        case 1: *counters = kOEpochCounters; *per = kOEpochPer; return MOA_SUCCESS;
+        case 2: *counters = kFfnEpochCounters; *per = kFfnEpochPer; return MOA_SUCCESS;
+    }
+    return fail(MOA_ERROR_INVALID_VALUE, "kernel must be 0 (QKV), 1 (O) or 2 (FFN)");
+}
+
+int moa_test_epoch_tag(int kernel, uint64_t old, uint32_t* tag) {
+    if (!tag) return fail(MOA_ERROR_INVALID_VALUE, "tag is NULL");
+    switch (kernel) {
+        case 0: *tag = epoch_tag<kQkvEpochPer>(old); return MOA_SUCCESS;
+        case 1: *tag = epoch_tag<kOEpochPer>(old); return MOA_SUCCESS;
+        case 2: *tag = epoch_tag<kFfnEpochPer>(old); return MOA_SUCCESS;
+    }
+    return fail(MOA_ERROR_INVALID_VALUE, "kernel must be 0 (QKV), 1 (O) or 2 (FFN)");
+}
+
+int moa_test_preset_epochs(uint64_t launches) {
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    hipError_t e = hipDeviceSynchronize();
+    auto put64 = [&](int first, int n, uint64_t v) {
+        for (int i = 0; i < n && e == hipSuccess; ++i)
+            e = hipMemcpy(ctx->tickets + (size_t)(first + i) * kTicketStride, &v, sizeof v, hipMemcpyHostToDevice);
+    };
+    put64(kTicketQkvEpoch, kQkvEpochCounters, launches * kQkvEpochPer);
+    put64(kTicketOEpoch, kOEpochCounters, launches * kOEpochPer);
+    put64(kTicketFfnEpoch, kFfnEpochCounters, launches * kFfnEpochPer);
+    const uint32_t at = (uint32_t)(launches * 32u);
+    for (int i = 0; i < kMaxDecodeM * kNs && e == hipSuccess; ++i)
+        e = hipMemcpy(ctx->tickets + (size_t)(kTicketAttn + i) * kTicketStride, &at, sizeof at, hipMemcpyHostToDevice);
+    return finish(e, "presetting the epoch counters");
 }
 
 int moa_format_selftest(uint32_t* out, void* stream) {

@@ -110,7 +110,8 @@ __device__ __forceinline__ int post_leader_row(int lane) {
 
 // One wave of leader workgroup g < kPostLeaders: poll until all 240 partial sums and the outputs of
 // workgroups g, g + 8, ... carry `tag`; sum the partials in a fixed order (the same bits in every
-// leader) and write those workgroups' residual rows in place:
+// leader) and write those workgroups' residual rows in place (nothing when the poll expired, so
+// rows are never computed from stale words):
 //   out = bf16(bf16(r + bf16(bf16(d * inv) * w)) * ls)    (ls skipped when has_ls is false)
 // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241. r8 / w8: the lane's residual and
 // norm-weight values (prefetched by the caller at post_leader_row).
@@ -122,6 +123,7 @@ __device__ __forceinline__ void post_leader(PostSlots* slots, uint32_t tag, uint
     const bool mine_rows = lane < 2 * kPostGroup;
     const int lwg = blockIdx.x + kPostLeaders * min(lane / 2, kPostGroup - 1);
     const uint64_t t0 = wall_clock64();
+    bool expired = false;
     for (;;) {
         bool ok = true;
 #pragma unroll
@@ -140,6 +142,7 @@ __device__ __forceinline__ void post_leader(PostSlots* slots, uint32_t tag, uint
         if (__all(ok)) break;
         if (wall_clock64() - t0 > kSpinTicks) {
             if (lane == 0) atomicOr(err, kErrSpinTimeout);
+            expired = true;
             break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -148,7 +151,7 @@ __device__ __forceinline__ void post_leader(PostSlots* slots, uint32_t tag, uint
 #pragma unroll
     for (int i = 0; i < NP; ++i) tot += part[i];
     const float inv = rms_inverse(wave_sum(tot), kH);
-    if (mine_rows) {
+    if (mine_rows && !expired) {
         const uint32_t rw[4] = {r8.x, r8.y, r8.z, r8.w}, ww[4] = {w8.x, w8.y, w8.z, w8.w};
         uint32_t o[4];
 #pragma unroll
@@ -513,7 +516,7 @@ __device__ __forceinline__ void qkv_head_epilogue(const QkvParams& p, const uint
     const int32_t kv_off = *p.kv_off;
     const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + m < kE;
     const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
-    if (!rope_ok || !kv_ok) {  // the call writes nothing (no q_out, K or V) on a bad offset
+    if (!rope_ok || !kv_ok) {  // this token row writes nothing (no q_out, K or V) on a bad offset
         if (t == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
         return;
     }
@@ -662,8 +665,8 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
 // h = b / 8 -- rows 16q .. 16q+15 and 128+16q .. 128+16q+15 of the head for q = b % 8, so every
 // row's RoPE partner (t ^ 128) is in the same workgroup. The head's RMSNorm needs the sum of
 // squares of all 256 rows: each workgroup publishes its partial sum tagged with the launch's
-// epoch (the head's epoch counter gets one add per workgroup at entry; the count read, divided
-// by 8, is the number of earlier launches) and polls the head's 8 tagged words. Then the
+// epoch (the head's epoch counter gets one add per workgroup at entry; epoch_tag) and polls the
+// head's 8 tagged words. Then the
 // control wave normalises, rotates and stores the workgroup's 32 values.
 constexpr int kQkvWaves = 8;                                // row waves; wave 8 is the control wave
 constexpr int kQkvBlock = 64 * (kQkvWaves + 1);
@@ -672,6 +675,7 @@ constexpr int kQkvWgRows = kQkvWaves * kQkvRowsW;           // 32
 constexpr int kQkvGrid = kQkvRows / kQkvWgRows;             // 256
 constexpr int kQkvPerHead = kDs / kQkvWgRows;               // 8 workgroups per head
 static_assert(kQkvPerHead * kQkvWgRows == kDs && kQkvGrid == 32 * kQkvPerHead, "QKV grid");
+static_assert(kQkvPerHead == kQkvEpochPer && kQkvEpochCounters == 32, "one epoch counter per head");
 static_assert(32 * kQkvPerHead == kQkvSlotWords, "one tagged word per workgroup");
 
 // Head-local row of slot s = 4 w + r (w < 4: first half of the head, w >= 4: second half).
@@ -698,7 +702,7 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
 
     // Control wave: offsets and norm weight at entry (ahead of every weight load, so waiting for
     // them later costs nothing); lane i < 32 serves head-local row qkv_local_row(q, i).
-    uint32_t ep = 0;
+    uint32_t tag = 0;
     float wv = 1.0f, cv = 0.0f, sv = 0.0f;
     int32_t rope_off = 0, kv_off = 0;
     const int te = qkv_local_row(q, min(lane, kQkvWgRows - 1));
@@ -740,7 +744,7 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
     // exchange, and loads retire in order -- issued first, the epoch add's return would hold up
     // every later wait of the wave.
     if (ctl) {
-        if (lane == 0) ep = counter_add(tickets + (kTicketQkvEpoch + head) * kTicketStride) / kQkvPerHead;
+        if (lane == 0) tag = epoch_tag<kQkvEpochPer>(epoch_add(tickets + (kTicketQkvEpoch + head) * kTicketStride));
         const int trow = rope_off / (kDs * 2) + m0;
         if (head < 24 && rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && trow < kE) {
             cv = bf2f(p.cos[(size_t)trow * kDs + te]);
@@ -776,7 +780,7 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
 
     // RMSNorm over the head (sliding/rmsnorm.rs:22-153): partial sum of this workgroup's 32 rows,
     // then the head's 8 partials in workgroup order.
-    const uint32_t tag = __shfl(ep, 0, kWave) + 1u;
+    tag = __shfl(tag, 0, kWave);
     uint64_t* hslots = slots + head * kQkvPerHead;
     if (lane == 0) {
         float ss = 0.0f;
@@ -790,9 +794,9 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
         const uint64_t v = collect64(hslots + min(lane, kQkvPerHead - 1));
         part = __uint_as_float((uint32_t)v);
         if (__all(lane >= kQkvPerHead || (uint32_t)(v >> 32) == tag)) break;
-        if (wall_clock64() - tp > kSpinTicks) {
+        if (wall_clock64() - tp > kSpinTicks) {  // expired: store nothing rather than stale values
             if (lane == 0) atomicOr(err, kErrSpinTimeout);
-            break;
+            return;
         }
         __builtin_amdgcn_s_sleep(1);
     }
@@ -803,7 +807,7 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
 
     const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + m0 < kE;
     const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
-    if (!rope_ok || !kv_ok) {  // the call writes nothing (no q_out, K or V) on a bad offset
+    if (!rope_ok || !kv_ok) {  // this token row writes nothing (no q_out, K or V) on a bad offset
         if (blockIdx.x == 0 && lane == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
         return;
     }
@@ -901,14 +905,12 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
 // weight loads behind it (a CU serves its loads in order); the wave's two rows (8 KB) then go out
 // at once. Outputs and partial sums of squares leave through the tagged post-norm hand-off; the
 // kPostLeaders leaders apply post-norm and residual. The tag is the launch's epoch: the control
-// wave of workgroup b adds one to epoch counter b % 16 at entry (15 workgroups per counter), and
-// the count it reads, divided by 15, is the number of earlier launches.
+// wave of workgroup b adds one to epoch counter b % 15 (16 workgroups per counter; epoch_tag).
 constexpr int kOWaves = 8;
 constexpr int kOBlock = 64 * kOWaves;
 constexpr int kORowsW = 2;  // rows per wave
-constexpr int kOEpochCounters = 16;
 static_assert(kPostGrid * kPostWgRows == kH && kOWaves * kORowsW == kPostWgRows, "O grid");
-static_assert(kPostGrid % kOEpochCounters == 0, "equal workgroups per epoch counter");
+static_assert(kPostGrid == kOEpochCounters * kOEpochPer, "equal workgroups per epoch counter");
 
 template <ScaleKind SK, int KX>
 __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, PostSlots* slots, uint32_t* tickets,
@@ -920,7 +922,7 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
     const bool leader = blockIdx.x < kPostLeaders;
     uint16_t* res = p.residual + (size_t)m0 * kH;
 
-    uint32_t ep = 0;
+    uint32_t tag = 0;
     uint4 r8 = make_uint4(0, 0, 0, 0), w8 = make_uint4(0, 0, 0, 0);
     if (ctl) {
         if (leader) {
@@ -945,8 +947,7 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
     // the epoch add behind the weights (loads retire in order: issued first, its return would
     // hold up every later wait of the wave)
     if (ctl && lane == 0)
-        ep = counter_add(tickets + (kTicketOEpoch + blockIdx.x % kOEpochCounters) * kTicketStride) /
-             (kPostGrid / kOEpochCounters);
+        tag = epoch_tag<kOEpochPer>(epoch_add(tickets + (kTicketOEpoch + blockIdx.x % kOEpochCounters) * kTicketStride));
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
         const int k = (threadIdx.x + i * kOBlock) * 8;
@@ -973,7 +974,7 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
     if (lane < kORowsW) dl[wave * kORowsW + lane] = f2bf(mine * scale);  // generate_references.py:265-274
     __syncthreads();
     if (!ctl) return;
-    const uint32_t tag = __shfl(ep, 0, kWave) + 1u;
+    tag = __shfl(tag, 0, kWave);
     post_publish(slots, tag, dl, lane);
     if (!leader) return;
     post_leader(slots, tag, res, r8, w8, false, 1.0f, lane, err);
@@ -1134,9 +1135,9 @@ __device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnPa
 // until they do. No atomic arrival or poll sits between the last workgroup's up/gate rows and
 // everyone's p. (FP4 weights used an arrival-tree barrier here before; the tagged words measured
 // 0.2-0.35 us faster.)
-// The launch's tag is ep + 1: 16 counters, each advanced by 15 workgroups per launch of any format,
-// give ep. Tags therefore never repeat across launches, so a word left by an earlier launch never
-// carries the current tag.
+// The launch's tag: 15 epoch counters, each advanced by 16 workgroups per launch of any format
+// (epoch_tag). Consecutive launches never share a tag, so a word left by an earlier launch does
+// not carry the current one.
 //
 // Post-norm: every workgroup publishes its 16 down outputs and its partial sum of squares, each
 // 64-bit word carrying the launch's tag (a word holding the tag is complete, so no counters), and
@@ -1154,7 +1155,7 @@ constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
 constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
 constexpr int kFfnDownPre = 4;                      // down chunks per row loaded before p is staged (FP8)
 constexpr int kFfnDownPreFp4 = 4;                   // the same for FP4 rows (8 chunks; measured: 2 equal, 6 and 8 slower)
-constexpr int kFfnEpochCounters = 16;               // launch-epoch counters (15 workgroups each)
+static_assert(kFfnGrid == kFfnEpochCounters * kFfnEpochPer, "equal workgroups per epoch counter");
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
 static_assert(kFfnGrid == kPostGrid && kFfnWgRows == kPostWgRows, "post-norm hand-off shape");
 
@@ -1173,16 +1174,16 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
     __shared__ float red[kFfnWaves];
     __shared__ float pl[kFfnWaves * kUgRL];
     __shared__ uint32_t dl[kFfnWgRows];  // the workgroup's down outputs (bf16 bits)
-    __shared__ uint32_t s_tag;
+    __shared__ uint32_t s_tag, s_expired;
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
     const bool leader = blockIdx.x < kPostLeaders;
-    // The launch's tag: 16 counters of 15 workgroups each advance by one per launch (every format
-    // shares them, so post-norm slot tags never repeat across formats). Needed only after up/gate.
-    uint32_t ep = 0;
+    // The launch's tag: 15 counters of 16 workgroups each advance by one block per launch (every
+    // format shares them, so post-norm slot tags never repeat across formats). Needed only after
+    // up/gate.
+    uint32_t ep_tag = 0;
     if (ctl && lane == 0)
-        ep = counter_add(tickets + (kTicketFfnEpoch + blockIdx.x % kFfnEpochCounters) * kTicketStride) /
-             (kFfnGrid / kFfnEpochCounters);
+        ep_tag = epoch_tag<kFfnEpochPer>(epoch_add(tickets + (kTicketFfnEpoch + blockIdx.x % kFfnEpochCounters) * kTicketStride));
     uint16_t* res = p.residual + (size_t)m0 * kH;
     const bool post = p.post_rms != nullptr;
 
@@ -1208,7 +1209,10 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
     const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
     const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red);
     if (lane < kUgRL) pl[lane * kFfnWaves + wave] = pv;
-    if (ctl && lane == 0) s_tag = ep + 1u;
+    if (ctl && lane == 0) {
+        s_tag = ep_tag;
+        s_expired = 0u;
+    }
     __syncthreads();  // pl complete; every wave has read its x out of sh
     const uint32_t tag = s_tag;
 
@@ -1245,7 +1249,10 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
             for (int i = 0; i < PW; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
             if (__all(ok)) break;
             if (wall_clock64() - t0 > kSpinTicks) {
-                if (lane == 0) atomicOr(err, kErrSpinTimeout);
+                if (lane == 0) {
+                    atomicOr(err, kErrSpinTimeout);
+                    s_expired = 1u;
+                }
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -1282,7 +1289,9 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         if (lane < kFfnDownR) dl[wave * kFfnDownR + lane] = f2bf(proj_commit<F>(mine, dscale));
     }
     __syncthreads();  // dl complete
-    if (!ctl) return;
+    // A workgroup whose wait for p expired has computed from stale words: it stores and publishes
+    // nothing, so its residual rows keep their input values (and the leaders' polls expire too).
+    if (!ctl || s_expired) return;
 
     // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241: out = bf16(bf16(r + n) * ls),
     // n = bf16(bf16(d * inv) * w) with the post-norm, n = d without it.

@@ -26,11 +26,15 @@ constexpr int kTreeLeaves = 16;
 constexpr int kTreeCounters = kTreeLeaves + 1;
 constexpr int kTicketQkv = 0;
 constexpr int kTicketO = kTicketQkv + 32 * kMaxDecodeM;
-// Epoch counters of the single-launch O (16) and QKV (one per head) kernels: monotonic, never
-// reset; a workgroup adds one at entry and divides what it read by the workgroups per counter.
+// 64-bit epoch counters of the single-launch O (15 counters of 16 workgroups), QKV (one per head,
+// 8 workgroups) and FFN (15 of 16) kernels: monotonic, never reset; a workgroup adds one at entry
+// and divides what it read by the workgroups per counter (epoch_tag, moa_sync.h).
 constexpr int kTicketOEpoch = kTicketO + kTreeCounters * kMaxDecodeM;
 constexpr int kTicketQkvEpoch = kTicketOEpoch + 16;
-constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;  // 16 counters, 15 FFN workgroups each
+constexpr int kTicketFfnEpoch = kTicketQkvEpoch + 32;
+constexpr int kOEpochCounters = 15, kOEpochPer = 16;
+constexpr int kQkvEpochCounters = 32, kQkvEpochPer = 8;
+constexpr int kFfnEpochCounters = 15, kFfnEpochPer = 16;
 // sliding_attention: one counter per (row, head) of a launch, 32 arrivals per launch, never reset
 constexpr int kTicketAttn = kTicketFfnEpoch + 16;
 constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;

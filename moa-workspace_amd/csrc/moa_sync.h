@@ -39,6 +39,24 @@ __device__ __forceinline__ uint4 collect16(const uint16_t* p) {
 __device__ __forceinline__ uint32_t counter_add(uint32_t* c) {
     return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Launch epochs of the single-launch kernels. An epoch counter is a 64-bit word that each of a
+// fixed number `per` (a power of two) of the launch's workgroups advances by one at entry, and
+// the value a workgroup reads, divided by `per`, is the number of earlier launches. Because
+// every launch adds exactly `per`, all workgroups of one launch read values in the same block
+// of `per`, and 64 bits never wrap. The launch's tag is that count modulo 2^32 - 1, plus one:
+// 1 .. 2^32 - 1, never 0 (the value of a zero-filled slot), and consecutive launches always
+// differ. A tagged word is rewritten by every launch that reads it, so a word left by an
+// earlier launch never carries the current tag (a word skipped by 2^32 - 2 launches in a row
+// could: the FFN's post-norm words when no post-norm is asked for that many times).
+__device__ __forceinline__ uint64_t epoch_add(uint32_t* c) {
+    return __hip_atomic_fetch_add(reinterpret_cast<uint64_t*>(c), 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <int per>
+__host__ __device__ __forceinline__ uint32_t epoch_tag(uint64_t old) {
+    static_assert(per > 0 && (per & (per - 1)) == 0, "a power of two of workgroups per epoch counter");
+    return (uint32_t)((old / per) % 0xffffffffull) + 1u;
+}
 __device__ __forceinline__ void counter_reset(uint32_t* c) {
     __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

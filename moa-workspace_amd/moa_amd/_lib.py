@@ -72,6 +72,11 @@ SIGNATURES = {
     "moa_decoder_feedforward_mxfp4": [P] * 10 + [I32, P],
     "moa_fp8_scaled_projection": [P] * 4 + [I32, I32, I32, P],
     "moa_format_selftest": [P, P],
+    "moa_test_epoch_layout": [I32, C.POINTER(C.c_int), C.POINTER(C.c_int)],
+    "moa_test_epoch_tag": [I32, U64, U32P],
+    "moa_test_preset_epochs": [U64],
+    # include/moa_bench.h
+    "moa_bench_stream_read": [P, U64, I32, I32, P, P],
 }
 _RESTYPES = {"moa_version": C.c_char_p, "moa_last_error_string": C.c_char_p}
 

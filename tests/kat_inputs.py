@@ -257,13 +257,24 @@ def ffn_stress_inputs() -> dict:
     return out
 
 
+def sign_failures(expected_f32: np.ndarray, actual_f32: np.ndarray, atol: float) -> np.ndarray:
+    """BASELINE's "no sign-cancellation failures": where the expected value is at least atol in
+    magnitude, the output must carry its sign. (The atol/rtol bound alone lets an output flip sign
+    when |e| lies in [atol, atol / (1 - rtol)).) Returns the mask of failing elements."""
+    e = np.asarray(expected_f32, np.float32).reshape(-1)
+    a = np.asarray(actual_f32, np.float32).reshape(-1)
+    return (np.abs(e) >= atol) & (np.signbit(a) != np.signbit(e)) & (a != 0)
+
+
 def compare(expected_f32: np.ndarray, actual_bits: np.ndarray, atol: float, rtol: float = 1e-2):
     """The reference's gate (FO/src/bin/test_kernels.rs:626-671): every element finite and
-    |a - e| <= atol + rtol |e|. Returns (ok, max_abs_diff, n_exact, n_fail)."""
+    |a - e| <= atol + rtol |e|; plus the sign rule of sign_failures (a non-zero output of the
+    wrong sign where |e| >= atol fails, and so does a zero output there: it fails the bound).
+    Returns (ok, max_abs_diff, n_exact, n_fail)."""
     e = np.asarray(expected_f32, np.float32).reshape(-1)
     a = unbf(np.asarray(actual_bits).reshape(-1).view(np.uint16))
     if not np.all(np.isfinite(a)):
         return False, float("inf"), 0, int(np.count_nonzero(~np.isfinite(a)))
     diff = np.abs(a - e)
-    fail = diff > atol + rtol * np.abs(e)
+    fail = (diff > atol + rtol * np.abs(e)) | sign_failures(e, a, atol)
     return (not fail.any()), float(diff.max(initial=0.0)), int(np.count_nonzero(diff == 0)), int(fail.sum())

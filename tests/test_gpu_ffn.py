@@ -78,8 +78,10 @@ def test_nvfp4_stress_known_answer():
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("run", range(3))
+@pytest.mark.parametrize("run", range(9))
 def test_nvfp4_reference_runs(run):
+    """The reference harness's runs 0-2 (FO/src/bin/test_kernels.rs:168) and the extra runs 3-8 of
+    its development sweep (moa-dev/extra_seeds.py:25,103-110: same names, RUN_OFFSET 3)."""
     need_gpu()
     say(f"ffn nvfp4 reference run {run}")
     d = synth.ref_ffn_inputs(run)
@@ -91,10 +93,13 @@ def cfg0():
     return synth.cfg_ffn_fp8(0)
 
 
-def test_fp8_config0(cfg0):
+@pytest.mark.parametrize("seed", range(3))
+def test_fp8_config0(seed, cfg0):
+    """BASELINE config 0 (the headline case) at M = 1, three seeds."""
     need_gpu()
-    say("ffn fp8 cfg0 seed0")
-    gate(oracle_fp8(cfg0), gpu_fp8(cfg0), "ffn fp8 cfg0", atol=FFN_ATOL)
+    say(f"ffn fp8 cfg0 seed{seed}")
+    d = cfg0 if seed == 0 else synth.cfg_ffn_fp8(seed)
+    gate(oracle_fp8(d), gpu_fp8(d), f"ffn fp8 cfg0 seed{seed}", atol=FFN_ATOL)
 
 
 def test_fp8_config0_literal_without_post_norm_and_gate(cfg0):
@@ -120,6 +125,50 @@ def test_mxfp4_config3(M):
     gate(oracle_mxfp4(d), gpu_mxfp4(d), f"ffn mxfp4 M{M}", atol=FFN_ATOL)
 
 
+def cancel_fp4_codes(packed: np.ndarray) -> np.ndarray:
+    """E2M1 rows whose elements 480k and 480k + 1 (the two nibbles of byte 240k, inside one block
+    scale in both FP4 formats) carry the same code, as full-ffn-stress builds its rows from
+    repeated codes (full-ffn-stress/generate_reference.py:44-60): weighted +a and -a, the
+    normalised cancelling pair contributes exactly zero in every row."""
+    w = packed.copy()
+    lo = w[:, 0::240] & 0x0F
+    w[:, 0::240] = lo | (lo << 4)
+    return w
+
+
+def cancellation_probe(d: dict, tiny_pow: int, fp8: bool) -> dict:
+    """The probe applied to one FFN case: residual [+1, -1, 478 x 2^p] per 480, unit pre-norm
+    weight, and up/gate rows that weight the pair equally."""
+    d = dict(d)
+    d["residual"] = cancellation_residual(tiny_pow)[None, :]
+    d["pre_ff_rms_weight"] = np.full(3840, 0x3F80, np.uint16)
+    for k in ("up", "gate"):
+        if fp8:
+            w = d[f"{k}_weight"].copy()
+            w[:, 0::480] = 0x38  # 1.0
+            w[:, 1::480] = 0x38
+            d[f"{k}_weight"] = w
+        else:
+            d[f"{k}_weight_packed"] = cancel_fp4_codes(d[f"{k}_weight_packed"])
+    return d
+
+
+def assert_geglu_near_zero(d: dict, fmt: int, label: str, bound: float = 1e-2) -> float:
+    """The oracle's GeGLU row p of a probe really is near zero (the pair cancelled): returns max |p|."""
+    keys = ("up_weight", "gate_weight", "down_weight") if fmt == O.FFN_FP8 else \
+        ("up_weight_packed", "gate_weight_packed", "down_weight_packed")
+    g = (d["up_global_scale"][0], d["gate_global_scale"][0], d["down_global_scale"][0]) if fmt == O.FFN_NVFP4 \
+        else (1.0, 1.0, 1.0)
+    w = O.ffn_weights(fmt, *[d[k] for k in keys], d["up_weight_scale"], d["gate_weight_scale"], d["down_weight_scale"],
+                      g)
+    h = O.rmsnorm(np.ascontiguousarray(d["residual"]), d["pre_ff_rms_weight"])
+    p = unbf(O.ffn_up_gate(h, w))
+    mp = float(np.abs(p).max())
+    say(f"[{label:40}] oracle max|GeGLU| = {mp:.3e}")
+    assert mp < bound, f"{label}: the probe did not cancel (max |p| {mp})"
+    return mp
+
+
 def cancellation_residual(tiny_pow: int) -> np.ndarray:
     """residual chunk [+1, -1, 478 x 2^p] per 480 (the QKV probe's construction,
     qkv-boundary-probe-e53/generate_suite.py:48-49): after the pre-norm the large pair cancels
@@ -130,20 +179,17 @@ def cancellation_residual(tiny_pow: int) -> np.ndarray:
 
 
 @pytest.mark.parametrize("tiny_pow", [-23, -12])
-def test_fp8_and_mxfp4_cancellation_probes(tiny_pow):
-    """up . gelu(gate) partial sums near zero: up/gate rows weight the cancelling pair with +1,+1."""
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "nvfp4"])
+def test_cancellation_probes(fmt, tiny_pow):
+    """BASELINE config 3's cancellation probe (and the same in FP8 and NVFP4): up . gelu(gate)
+    partial sums near zero, asserted on the oracle's GeGLU row before the kernel is compared."""
     need_gpu()
-    say(f"ffn cancellation probe 2^{tiny_pow}")
-    d = synth.cfg_ffn_fp8(4)
-    d["residual"] = cancellation_residual(tiny_pow)[None, :]
-    d["pre_ff_rms_weight"] = np.full(3840, 0x3F80, np.uint16)
-    for k in ("up_weight", "gate_weight"):
-        w = d[k].copy()
-        w[:, 0::480] = 0x38  # 1.0
-        w[:, 1::480] = 0x38
-        d[k] = w
-    gate(oracle_fp8(d), gpu_fp8(d), f"ffn fp8 cancel 2^{tiny_pow}", atol=FFN_ATOL)
-    m = synth.cfg_ffn_mxfp4(4)
-    m["residual"] = d["residual"]
-    m["pre_ff_rms_weight"] = d["pre_ff_rms_weight"]
-    gate(oracle_mxfp4(m), gpu_mxfp4(m), f"ffn mxfp4 cancel 2^{tiny_pow}", atol=FFN_ATOL)
+    say(f"ffn {fmt} cancellation probe 2^{tiny_pow}")
+    base = {"fp8": lambda: synth.cfg_ffn_fp8(4), "mxfp4": lambda: synth.cfg_ffn_mxfp4(4),
+            "nvfp4": lambda: synth.ref_ffn_inputs(4)}[fmt]()
+    d = cancellation_probe(base, tiny_pow, fmt == "fp8")
+    assert_geglu_near_zero(d, {"fp8": O.FFN_FP8, "mxfp4": O.FFN_MXFP4, "nvfp4": O.FFN_NVFP4}[fmt],
+                           f"ffn {fmt} cancel 2^{tiny_pow}")
+    want, got = {"fp8": (oracle_fp8, gpu_fp8), "mxfp4": (oracle_mxfp4, gpu_mxfp4),
+                 "nvfp4": (oracle_nvfp4, gpu_nvfp4)}[fmt]
+    gate(want(d), got(d), f"ffn {fmt} cancel 2^{tiny_pow}", atol=FFN_ATOL)

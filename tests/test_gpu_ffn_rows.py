@@ -9,8 +9,9 @@ import pytest
 
 from gpu_util import gate, gate_addend, need_gpu, say
 from moa_amd import synth
-from test_gpu_ffn import (FFN_ATOL, cancellation_residual, gpu_fp8, gpu_mxfp4, gpu_nvfp4, oracle_fp8, oracle_mxfp4,
-                          oracle_nvfp4)
+from oracle import oracle as O
+from test_gpu_ffn import (FFN_ATOL, assert_geglu_near_zero, cancel_fp4_codes, cancellation_residual, gpu_fp8, gpu_mxfp4,
+                          gpu_nvfp4, oracle_fp8, oracle_mxfp4, oracle_nvfp4)
 
 pytestmark = pytest.mark.gpu
 H = 3840
@@ -73,22 +74,28 @@ def test_rows_without_post_norm_and_layer_scalar():
                 atol=FFN_ATOL)
 
 
-@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
-def test_rows_cancellation_probe(fmt):
+@pytest.mark.parametrize("M", [4, 16])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4", "nvfp4"])
+def test_rows_cancellation_probe(fmt, M):
     """Rows whose pre-normed activations cancel in every up/gate row (the config-3 probe), mixed
-    with ordinary rows."""
+    with ordinary rows; the probe rows' GeGLU values are asserted near zero on the oracle."""
     need_gpu()
-    say(f"ffn rows {fmt} cancellation probe M4")
+    say(f"ffn rows {fmt} cancellation probe M{M}")
     want, got = FORMATS[fmt]
-    d = case(fmt, 4, "cancel")
+    d = case(fmt, M, "cancel")
     d["residual"] = d["residual"].copy()
     d["residual"][1] = cancellation_residual(-23)
     d["residual"][3] = cancellation_residual(-12)
     d["pre_ff_rms_weight"] = np.full(H, 0x3F80, np.uint16)
-    if fmt == "fp8":
-        for k in ("up_weight", "gate_weight"):
-            w = d[k].copy()
+    for k in ("up", "gate"):
+        if fmt == "fp8":
+            w = d[f"{k}_weight"].copy()
             w[:, 0::480] = 0x38  # 1.0
             w[:, 1::480] = 0x38
-            d[k] = w
-    gate(want(d), got(d), f"ffn rows {fmt} cancel M4", atol=FFN_ATOL)
+            d[f"{k}_weight"] = w
+        else:
+            d[f"{k}_weight_packed"] = cancel_fp4_codes(d[f"{k}_weight_packed"])
+    probes = dict(d, residual=np.ascontiguousarray(d["residual"][[1, 3]]))
+    assert_geglu_near_zero(probes, {"fp8": O.FFN_FP8, "mxfp4": O.FFN_MXFP4, "nvfp4": O.FFN_NVFP4}[fmt],
+                           f"ffn rows {fmt} cancel M{M}")
+    gate(want(d), got(d), f"ffn rows {fmt} cancel M{M}", atol=FFN_ATOL)
