@@ -138,6 +138,22 @@ int moa_decoder_feedforward_fp8(uint16_t* residual, const uint16_t* pre_ff_rms_w
                                 const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
                                 int M, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same operator as
+ * moa_decoder_feedforward_fp8, the same kernels and the same bits, for 1 <= M <= 16 rows (larger
+ * M is rejected with MOA_ERROR_INVALID_VALUE). Its scratch (about 1.9 MB: epoch counters,
+ * hand-off words, normalised rows, GeGLU rows, down partial sums) is a static device array that
+ * each GPU holds until the process ends; neither this call nor its set-up (first call on a
+ * device, or moa_init) allocates. Every call on one device shares that array and it keeps the
+ * last call's contents: calls that overlap on one device (different streams, no dependency)
+ * race. Independent of the scratch of the other entry points. */
+int moa_decoder_feedforward_fp8_noalloc(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                                        const uint8_t* up_weight, const uint8_t* gate_weight,
+                                        const uint8_t* down_weight, const float* up_weight_scale,
+                                        const float* gate_weight_scale, const float* down_weight_scale,
+                                        const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
+                                        int M, void* stream);
+
 /* GeGLU FFN with MXFP4 weights: E2M1 two per byte (as NVFP4) with E8M0 scales per 32
  * K-elements (up/gate [15360,120], down [3840,480]); no global scale. Same contract
  * otherwise; post_ff_rms_weight and layer_scalar may be NULL. */

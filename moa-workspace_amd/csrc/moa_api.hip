@@ -90,6 +90,73 @@ DevCtx* device_context(hipError_t* err) {
     return &c;
 }
 
+// ------------------------------------------------------------ the no-allocation entry point
+// moa_decoder_feedforward_fp8_noalloc runs the same kernels as moa_decoder_feedforward_fp8 for
+// 1..kMaxDecodeM rows, with every byte of scratch carved from `scratch` below instead of the
+// hipMalloc'd per-device block: the epoch counters and hand-off words of the one-token kernel,
+// and the normalised rows, GeGLU rows and down partial sums of the rows path. `scratch` is a
+// static device array, so each GPU holds its own copy from the moment the code object loads
+// (zero-filled, as static storage is) until the process ends. Its host-side name is not a device
+// address: the set-up below asks HIP for the device address once per device and only that
+// address ever reaches a kernel.
+namespace {
+constexpr size_t kNaTicketBytes = sizeof(uint32_t) * kTicketCount * kTicketStride;
+constexpr size_t kNaErrBytes = 256;
+constexpr size_t kNaPartBytes = sizeof(uint64_t) * kFfnSlotWords;
+constexpr size_t kNaPtagBytes = sizeof(uint64_t) * (kL / 2);
+constexpr size_t kNaHBytes = sizeof(uint16_t) * kMaxDecodeM * kH;
+constexpr size_t kNaPBytes = sizeof(uint16_t) * kMaxDecodeM * kL;
+constexpr size_t kNaFBytes = sizeof(float) * 4 * kMaxDecodeM * kH;  // 4 down splits of the rows path
+constexpr size_t na_up(size_t v) { return (v + 255) / 256 * 256; }
+constexpr size_t kNaTicketOff = 0;
+constexpr size_t kNaErrOff = kNaTicketOff + na_up(kNaTicketBytes);
+constexpr size_t kNaPartOff = kNaErrOff + na_up(kNaErrBytes);
+constexpr size_t kNaPtagOff = kNaPartOff + na_up(kNaPartBytes);
+constexpr size_t kNaHOff = kNaPtagOff + na_up(kNaPtagBytes);
+constexpr size_t kNaPOff = kNaHOff + na_up(kNaHBytes);
+constexpr size_t kNaFOff = kNaPOff + na_up(kNaPBytes);
+constexpr size_t kNaBytes = kNaFOff + na_up(kNaFBytes);  // 1.93 MB
+static_assert(kNaBytes < (2u << 20), "the no-allocation scratch stays under 2 MiB");
+
+static __device__ __align__(256) unsigned char scratch[kNaBytes];
+
+std::mutex g_na_mutex;
+DevCtx g_na_ctx[kMaxDevices];  // per device: pointers into that device's copy of `scratch`
+
+// Once per device, with that device current: the device address of its `scratch`, carved into a
+// context of the layout above. Allocates nothing. nullptr (and *code set) on failure.
+DevCtx* noalloc_context(int* code) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { *code = hip_fail(e, "hipGetDevice"); return nullptr; }
+    if (dev < 0 || dev >= kMaxDevices) { *code = fail(MOA_ERROR_NO_DEVICE, "device index out of range"); return nullptr; }
+    std::lock_guard<std::mutex> lock(g_na_mutex);
+    DevCtx& c = g_na_ctx[dev];
+    if (c.base) return &c;
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+        *code = hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+        return nullptr;
+    }
+    int cus = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) { *code = hip_fail(e, "hipDeviceGetAttribute"); return nullptr; }
+    char* b = static_cast<char*>(ptr);
+    c.device = dev;
+    c.cus = cus;
+    c.tickets = reinterpret_cast<uint32_t*>(b + kNaTicketOff);
+    c.err = reinterpret_cast<uint32_t*>(b + kNaErrOff);
+    c.ffn_part = reinterpret_cast<uint64_t*>(b + kNaPartOff);
+    c.ffn_ptag = reinterpret_cast<uint64_t*>(b + kNaPtagOff);
+    c.hbuf = reinterpret_cast<uint16_t*>(b + kNaHOff);
+    c.pbuf = reinterpret_cast<uint16_t*>(b + kNaPOff);
+    c.fbuf = reinterpret_cast<float*>(b + kNaFOff);
+    c.base = ptr;
+    return &c;
+}
+}  // namespace
+
 }  // namespace moa
 
 using namespace moa;
@@ -226,7 +293,8 @@ int moa_init(int device) {
     e = hipSetDevice(device);
     if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
     int code = MOA_SUCCESS;
-    return ctx_or_fail(&code) ? MOA_SUCCESS : code;
+    if (!ctx_or_fail(&code)) return code;
+    return noalloc_context(&code) ? MOA_SUCCESS : code;
 }
 
 int moa_device_errors(void* stream, uint32_t* bits) {
@@ -235,12 +303,20 @@ int moa_device_errors(void* stream, uint32_t* bits) {
     DevCtx* ctx = ctx_or_fail(&code);
     if (!ctx) return code;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    uint32_t host = 0;
-    hipError_t e = hipMemcpyAsync(&host, ctx->err, sizeof host, hipMemcpyDeviceToHost, s);
+    // the no-allocation entry point's error word too, once its scratch is set up on this device
+    const DevCtx* na = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_na_mutex);
+        if (g_na_ctx[ctx->device].base) na = &g_na_ctx[ctx->device];
+    }
+    uint32_t host[2] = {0, 0};
+    hipError_t e = hipMemcpyAsync(&host[0], ctx->err, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipMemsetAsync(ctx->err, 0, sizeof(uint32_t), s);
+    if (e == hipSuccess && na) e = hipMemcpyAsync(&host[1], na->err, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess && na) e = hipMemsetAsync(na->err, 0, sizeof(uint32_t), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "reading device error bits");
-    *bits = host;
+    *bits = host[0] | host[1];
     return MOA_SUCCESS;
 }
 
@@ -306,6 +382,25 @@ int moa_decoder_feedforward_fp8(uint16_t* residual, const uint16_t* pre_ff_rms_w
                 up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
                 nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
     return ffn_common(p, M, stream);
+}
+
+int moa_decoder_feedforward_fp8_noalloc(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
+                                        const uint8_t* up_weight, const uint8_t* gate_weight,
+                                        const uint8_t* down_weight, const float* up_weight_scale,
+                                        const float* gate_weight_scale, const float* down_weight_scale,
+                                        const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
+                                        int M, void* stream) {
+    FfnParams p{FfnFormat::FP8, residual, pre_ff_rms_weight, up_weight, gate_weight, down_weight,
+                up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
+    if (const int bad = ffn_check(p, M)) return bad;
+    if (M > kMaxDecodeM)
+        return fail(MOA_ERROR_INVALID_VALUE, "M must be in [1, " + std::to_string(kMaxDecodeM) +
+                                                 "] for the no-allocation entry point, got " + std::to_string(M));
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = noalloc_context(&code);
+    if (!ctx) return code;
+    return finish(launch_ffn_decode(p, M, static_cast<hipStream_t>(stream), ctx), "decoder_feedforward_fp8_noalloc launch");
 }
 
 int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms_weight,

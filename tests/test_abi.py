@@ -44,6 +44,7 @@ def _null(n):
     ("moa_decoder_feedforward", 13, (1, None)),
     ("moa_decoder_feedforward_fp8", 10, (1, None)),
     ("moa_decoder_feedforward_mxfp4", 10, (1, None)),
+    ("moa_decoder_feedforward_fp8_noalloc", 10, (1, None)),
     ("moa_sliding_attention", 5, (1, None)),
     ("moa_final_norm_and_logits", 4, (1, None)),
     ("moa_full_project_qkv", 15, (1, None)),
