@@ -1129,9 +1129,9 @@ __device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnPa
 // p: tagged words instead of a barrier. Every workgroup's control wave publishes the workgroup's
 // 64 GeGLU values as 32 64-bit words (two bf16 values and the launch's tag). It issues them before
 // any other load of the workgroup: a CU serves its loads in order, so the words are not queued
-// behind the workgroup's weight loads. Then every thread issues its first read of p (15 words;
-// workgroups start at different words so that they do not all request one line), and every wave
-// issues its first kFfnDownPre down chunks. Words that do not yet carry the tag are read again
+// behind the workgroup's weight loads. Then every wave issues its first kFfnDownPre down chunks,
+// and behind them every thread its first read of p (15 words; workgroups start at different words
+// so that they do not all request one line). Words that do not yet carry the tag are read again
 // until they do. No atomic arrival or poll sits between the last workgroup's up/gate rows and
 // everyone's p. (FP4 weights used an arrival-tree barrier here before; the tagged words measured
 // 0.2-0.35 us faster.)
@@ -1153,7 +1153,7 @@ constexpr int kFfnGrid = kL / (kFfnWaves * kUgRL);  // 240 workgroups
 constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgroup
 constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
 constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
-constexpr int kFfnDownPre = 4;                      // down chunks per row loaded before p is staged (FP8)
+constexpr int kFfnDownPre = 8;                      // down chunks per row loaded before p is staged (FP8; 6-10 measured alike, 12 spills)
 constexpr int kFfnDownPreFp4 = 4;                   // the same for FP4 rows (8 chunks; measured: 2 equal, 6 and 8 slower)
 static_assert(kFfnGrid == kFfnEpochCounters * kFfnEpochPer, "equal workgroups per epoch counter");
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
@@ -1226,8 +1226,8 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         // p by tagged words instead of a barrier. The control wave's 32 words (two GeGLU values and
         // the launch's tag each) are issued before any other load of the workgroup: a CU serves
         // its loads in order, so they are not queued behind this workgroup's weight loads. Every
-        // thread then issues its first read of p, then every wave (the control wave too) its
-        // first PD down chunks; words not yet current are read again until they are.
+        // wave (the control wave too) then issues its first PD down chunks and every thread its
+        // first read of p; words not yet current are read again until they are.
         if (ctl && lane < kFfnWaves * kUgRL / 2)
             publish64(ptag + blockIdx.x * (kFfnWaves * kUgRL / 2) + lane,
                       tagged(tag, f2bf(pl[2 * lane]) | (f2bf(pl[2 * lane + 1]) << 16)));
@@ -1237,11 +1237,15 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         // word w of thread t in read i: workgroups start at different words (rotation by 32 b), so
         // that 240 readers of the same 61 KB do not request the same lines at the same time
         auto pword = [&](int i) { return (threadIdx.x + kFfnBlock * i + blockIdx.x * 32) % (kL / 2); };
+        // The down prefetch goes out first and the reads of p behind it: a CU returns its loads in
+        // order, so a read of p issued ahead of the prefetch would come back early, find the words
+        // of the slowest workgroups not yet published, and its re-read would then queue behind the
+        // whole prefetch. Behind it, the first read lands when nearly every word is current.
+#pragma unroll
+        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
         uint64_t pw[PW];
 #pragma unroll
         for (int i = 0; i < PW; ++i) pw[i] = collect64(ptag + pword(i));
-#pragma unroll
-        for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
         const uint64_t t0 = wall_clock64();
         for (;;) {
             bool ok = true;
