@@ -222,6 +222,13 @@ def main() -> int:
         run_co(i)
         run_cffn(i)
 
+    if CM:
+        c_res_mx = dev(synth.bf16_normal("cfg4.mxfp4.residual", (CM, 3840)))
+
+    def run_cffn_mxfp4(i):
+        w = MXW[i % nmx]
+        ops.decoder_feedforward_mxfp4(c_res_mx, f_pre, *[w[k] for k in MXK], f_post, f_ls)
+
     def run_ffn(i):
         w = FW[i % nf]
         ops.decoder_feedforward_fp8(f_res, f_pre, w["up_weight"], w["gate_weight"], w["down_weight"],
@@ -362,9 +369,10 @@ def main() -> int:
     chunk = None
     if CM:
         chunk = {"rows": CM, "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "peak_fp8_TFLOPs": MFMA_FP8_PEAK_TFLOPS, "ops": {}}
-        for name, fn in (("qkv", run_cqkv), ("o", run_co), ("ffn", run_cffn), ("layer", run_layer)):
+        for name, fn in (("qkv", run_cqkv), ("o", run_co), ("ffn", run_cffn), ("layer", run_layer),
+                         ("ffn_mxfp4", run_cffn_mxfp4)):
             ms, p10, p90 = graph_stats(fn, calls=8, warmup=8, replays=10)
-            flops = CM * (sum(FLOPS_PER_ROW.values()) if name == "layer" else FLOPS_PER_ROW[name])
+            flops = CM * (sum(FLOPS_PER_ROW.values()) if name == "layer" else FLOPS_PER_ROW[name.split("_")[0]])
             tf = flops / (ms * 1e-3) / 1e12
             chunk["ops"][name] = {"us": round(ms * 1e3, 2), "us_p10": round(p10 * 1e3, 2), "us_p90": round(p90 * 1e3, 2),
                                   "us_per_token": round(ms * 1e3 / CM, 4), "TFLOPs": round(tf, 1),

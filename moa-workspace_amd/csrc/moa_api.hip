@@ -265,10 +265,8 @@ int ffn_common(const FfnParams& p, int M, void* stream) {
     DevCtx* ctx = ctx_or_fail(&code);
     if (!ctx) return code;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // More than kMaxDecodeM rows with FP8 weights take the MFMA path; FP4 formats stay on the
-    // per-row kernels (16 rows per launch).
-    if (M <= kMaxDecodeM || p.fmt != FfnFormat::FP8)
-        return finish(launch_ffn_decode(p, M, s, ctx), "decoder_feedforward launch");
+    // More than kMaxDecodeM rows take the MFMA path (every weight format).
+    if (M <= kMaxDecodeM) return finish(launch_ffn_decode(p, M, s, ctx), "decoder_feedforward launch");
     for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
         const int e = finish(launch_ffn_chunk(p, m0, M - m0 < kMaxChunkM ? M - m0 : kMaxChunkM, s, ctx),
                              "decoder_feedforward launch");

@@ -2,8 +2,10 @@
 //
 // A chunk of M <= kMaxChunkM rows turns each projection into a dense contraction
 // Y[M, N] = X[M, K] . W[N, K]^T, computed on the matrix cores: v_mfma_f32_32x32x16_bf16 with the
-// bf16 activations as A and the FP8 weights widened to bf16 (exact: every E4M3 value is a bf16
-// value) as B, f32 accumulation. The operators' row-wise steps run as small kernels around it:
+// bf16 activations as A and the weights widened to bf16 as B, f32 accumulation. The widening is
+// exact in every format: E4M3 values are bf16 values; an MXFP4 weight is an E2M1 value times a
+// power of two (its E8M0 block scale); an NVFP4 weight, E2M1 times its E4M3 block scale, has at
+// most six significant bits (generate_references.py:383-414 folds the same product into bf16). The operators' row-wise steps run as small kernels around it:
 //   QKV: RMSNorm rows -> one GEMM over [Wq; Wk; Wv] (bf16(acc * s)) -> per-head RMSNorm + RoPE +
 //        q_out / ring-cache stores
 //   O:   GEMM (split-K, f32 partials) -> d = bf16(sum * s) -> post-RMSNorm + residual
@@ -39,6 +41,31 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
     return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// 8 E2M1 codes (one dword, lower index in the low nibble) widened to 8 bf16 with their block
+// scale: MXFP4 -- the conversion applies the exponent field of its f32 scale, so the E8M0 code goes
+// into bits 23-30; NVFP4 -- each value times the E4M3 scale in f32 (exact: at most six significant
+// bits), whose high half is then the bf16.
+template <FfnFormat F>
+__device__ __forceinline__ bf16x8 fp4x8_to_bf16(uint32_t q, uint32_t sc) {
+    if constexpr (F == FfnFormat::MXFP4) {
+        const float s = __uint_as_float((sc & 0xffu) << 23);
+        const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, s, 0);
+        const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, s, 1);
+        const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, s, 2);
+        const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, s, 3);
+        return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    } else {
+        const float s = e4m3_to_f32(sc);
+        float v[8];
+        fp4x8_to_f32(q, 1.0f, v);
+        uint32_t u[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            u[i] = __builtin_amdgcn_perm(__float_as_uint(v[2 * i + 1] * s), __float_as_uint(v[2 * i] * s), 0x07060302u);
+        return __builtin_bit_cast(bf16x8, make_uint4(u[0], u[1], u[2], u[3]));
+    }
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
 // Activation layout of the MFMA path ("A tiles"): a row-major [M][K] bf16 matrix is stored as
@@ -71,6 +98,10 @@ struct GemmArgs {
     const uint8_t* w2;  // GeGLU: the gate matrix (w[0] is up); s[0], s2 their scales
     const void* s0;
     const void* s2;
+    const uint8_t* wsc[3];  // FP4 weights: block-scale codes of w[i] ([rows][K/16] NVFP4, [rows][K/32] MXFP4)
+    const uint8_t* wsc2;    // ... and of w2
+    const float* g0;        // NVFP4 GeGLU: reciprocal global scales of up (w[0]) and gate (w2), device
+    const float* g2;
     uint16_t* y;        // GeGLU: bf16 A tiles of [M][N] (the down projection's input)
     float* yf;          // F32Partial: [gridDim.z][M][N]
 };
@@ -104,8 +135,14 @@ constexpr int kCkNt = 2;  // cache policy: non-temporal (weights are read once)
 //   All loads are buffer loads whose per-lane offsets are fixed: the step moves the scalar
 //   offset only. Prefetches past the last step repeat the last step (harmless), so the loop body
 //   has no branches.
-template <Epi E, ScaleKind SK>
+template <Epi E, ScaleKind SK, FfnFormat F = FfnFormat::FP8>
 __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_gemm_kernel(GemmArgs g) {
+    constexpr bool FP4 = F != FfnFormat::FP8;
+    // bytes per weight row and per 64-k step; FP4 block-scale bytes per row and per step
+    const int rb = FP4 ? g.K / 2 : g.K;
+    constexpr int kStepB = FP4 ? kCkBK / 2 : kCkBK;
+    const int sb = F == FfnFormat::NVFP4 ? g.K / 16 : (F == FfnFormat::MXFP4 ? g.K / 32 : 0);
+    constexpr int kStepS = F == FfnFormat::NVFP4 ? 4 : 2;
     // three weight buffers during the loop; the GeGLU epilogue reuses the space for its transpose
     constexpr int kWsBytes = kCkBN * kCkWStride, kTpStride = 72;
     constexpr int kLds = 3 * kWsBytes > 4 * 64 * kTpStride * 2 ? 3 * kWsBytes : 4 * 64 * kTpStride * 2;
@@ -117,22 +154,36 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int m_wave = m_blk + wave * 64;
     const int kz = g.K / gridDim.z, kbeg = blockIdx.z * kz, nsteps = kz / kCkBK;
 
-    // staged weight rows of this thread: tile rows r0 and r0 + 64, 16 bytes at 16 q of each step
+    // staged weight rows of this thread: tile rows r0 and r0 + 64, k 16 q .. 16 q + 15 of each step
+    // (FP8: 16 bytes; FP4: 8 bytes of codes and the one block-scale code covering them)
     const int r0 = t >> 2, q = t & 3;
-    __amdgpu_buffer_rsrc_t wrs[2];
-    int wvo[2];
+    __amdgpu_buffer_rsrc_t wrs[2], srs[2];
+    int wvo[2], svo[2] = {0, 0};
+    const int kcol = FP4 ? (kbeg + 16 * q) / 2 : kbeg + 16 * q;
+    const int scol = F == FfnFormat::NVFP4 ? kbeg / 16 + q : kbeg / 32 + q / 2;
     int seg = 0;
     if constexpr (E == Epi::GeGLU) {
-        const size_t off = (size_t)blockIdx.x * 64 * g.K;
-        wrs[0] = ck_rsrc(g.w[0] + off, 64u * g.K);
-        wrs[1] = ck_rsrc(g.w2 + off, 64u * g.K);
-        wvo[0] = wvo[1] = r0 * g.K + kbeg + 16 * q;
+        const size_t off = (size_t)blockIdx.x * 64 * rb;
+        wrs[0] = ck_rsrc(g.w[0] + off, 64u * rb);
+        wrs[1] = ck_rsrc(g.w2 + off, 64u * rb);
+        wvo[0] = wvo[1] = r0 * rb + kcol;
+        if constexpr (FP4) {
+            const size_t so = (size_t)blockIdx.x * 64 * sb;
+            srs[0] = ck_rsrc(g.wsc[0] + so, 64u * sb);
+            srs[1] = ck_rsrc(g.wsc2 + so, 64u * sb);
+            svo[0] = svo[1] = r0 * sb + scol;
+        }
     } else {
         const int n0 = blockIdx.x * kCkBN;
         while (seg + 1 < g.nsegs && n0 >= g.nseg[seg + 1]) ++seg;
-        wrs[0] = wrs[1] = ck_rsrc(g.w[seg] + (size_t)(n0 - g.nseg[seg]) * g.K, (uint32_t)kCkBN * g.K);
-        wvo[0] = r0 * g.K + kbeg + 16 * q;
-        wvo[1] = (r0 + 64) * g.K + kbeg + 16 * q;
+        wrs[0] = wrs[1] = ck_rsrc(g.w[seg] + (size_t)(n0 - g.nseg[seg]) * rb, (uint32_t)kCkBN * rb);
+        wvo[0] = r0 * rb + kcol;
+        wvo[1] = (r0 + 64) * rb + kcol;
+        if constexpr (FP4) {
+            srs[0] = srs[1] = ck_rsrc(g.wsc[seg] + (size_t)(n0 - g.nseg[seg]) * sb, (uint32_t)kCkBN * sb);
+            svo[0] = r0 * sb + scol;
+            svo[1] = (r0 + 64) * sb + scol;
+        }
     }
     const int wdst0 = r0 * kCkWStride + 32 * q, wdst1 = (r0 + 64) * kCkWStride + 32 * q;
 
@@ -156,17 +207,33 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     uint4 ar[3][2][4];     // [set][32-row block][16 bytes]: A(s) in set s mod 3, loaded two steps ahead
     bf16x8 bb[2][4];       // B fragments: [set][MFMA j]
     const int last = nsteps - 1;
+    // FP4: .x, .y the 16 codes, .z the block-scale code
     auto load_w = [&](uint4 (&dst)[2], int s) {
-        const int so = min(s, last) * kCkBK;
-        dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[0], wvo[0], so, kCkNt));
-        dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[1], wvo[1], so, kCkNt));
+        const int so = min(s, last) * kStepB;
+        if constexpr (FP4) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(wrs[i], wvo[i], so, kCkNt);
+                dst[i].x = v[0];
+                dst[i].y = v[1];
+                dst[i].z = __builtin_amdgcn_raw_buffer_load_b8(srs[i], svo[i], min(s, last) * kStepS, 0);
+            }
+        } else {
+            dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[0], wvo[0], so, kCkNt));
+            dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[1], wvo[1], so, kCkNt));
+        }
     };
     auto store_w = [&](const uint4 (&src)[2], int buf) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             bf16x8* d = reinterpret_cast<bf16x8*>(&ws[buf][i ? wdst1 : wdst0]);
-            d[0] = fp8x8_to_bf16(src[i].x, src[i].y);
-            d[1] = fp8x8_to_bf16(src[i].z, src[i].w);
+            if constexpr (FP4) {
+                d[0] = fp4x8_to_bf16<F>(src[i].x, src[i].z);
+                d[1] = fp4x8_to_bf16<F>(src[i].y, src[i].z);
+            } else {
+                d[0] = fp8x8_to_bf16(src[i].x, src[i].y);
+                d[1] = fp8x8_to_bf16(src[i].z, src[i].w);
+            }
         }
     };
     auto load_a = [&](uint4 (&dst)[2][4], int s) {
@@ -214,6 +281,8 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         // per SIMD issues them while the MFMA runs); the A prefetch rides with fragment 0, the
         // weight staging (16 widenings, 4 LDS writes, 2 loads) with fragment 1.
         constexpr int kDsR = 0x100, kDsW = 0x200, kVmR = 0x020, kValu = 0x002, kMfma = 0x008;
+        constexpr int kWLoads = FP4 ? 4 : 2;                    // weight (and scale) loads per step
+        constexpr int kWValu = F == FfnFormat::NVFP4 ? 8 : 2;   // widening instructions per MFMA slot
         read_b(bb[1], cb, 1);
         load_a(ar[(c + 2) % 3], s + 2);
         mfma8(a, bb[0], Par<0>{});
@@ -236,15 +305,15 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
             __builtin_amdgcn_sched_group_barrier(kDsR, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(kValu, 2, 1);
+            __builtin_amdgcn_sched_group_barrier(kValu, kWValu, 1);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(kValu, 2, 1);
+            __builtin_amdgcn_sched_group_barrier(kValu, kWValu, 1);
             __builtin_amdgcn_sched_group_barrier(kDsW, 1, 1);
         }
-        __builtin_amdgcn_sched_group_barrier(kVmR, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(kVmR, kWLoads, 1);
         __builtin_amdgcn_sched_barrier(0);
         read_b(bb[1], cb, 3);
         mfma8(a, bb[0], Par<2>{});
@@ -309,16 +378,29 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         // wave's own 9 KB of LDS (row stride 72 elements) so that each lane then stores whole
         // 16-byte units of the A tiles (row, 8 consecutive columns).
         uint16_t* tp = reinterpret_cast<uint16_t*>(smem) + wave * (64 * kTpStride);
+        // the format's commit of each projection: FP8 bf16(sum * s[n]); NVFP4 bf16(bf16(sum) * 1/g);
+        // MXFP4 bf16(sum) (generate_references.py:265-274, 358-372)
+        const float gu = F == FfnFormat::NVFP4 ? *g.g0 : 1.0f, gg = F == FfnFormat::NVFP4 ? *g.g2 : 1.0f;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const int n = blockIdx.x * 64 + nb * 32 + l32;
-            const float su = chunk_scale<SK>(g.s0, n), sg = chunk_scale<SK>(g.s2, n);
+            const float su = FP4 ? 1.0f : chunk_scale<SK>(g.s0, n), sg = FP4 ? 1.0f : chunk_scale<SK>(g.s2, n);
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int ml = 32 * mb + 8 * (r >> 2) + 4 * hf + (r & 3);
-                    const float up = rbf(acc[mb][nb][r] * su), gate = rbf(acc[mb][nb + 2][r] * sg);
+                    float up, gate;
+                    if constexpr (F == FfnFormat::FP8) {
+                        up = rbf(acc[mb][nb][r] * su);
+                        gate = rbf(acc[mb][nb + 2][r] * sg);
+                    } else if constexpr (F == FfnFormat::NVFP4) {
+                        up = rbf(rbf(acc[mb][nb][r]) * gu);
+                        gate = rbf(rbf(acc[mb][nb + 2][r]) * gg);
+                    } else {
+                        up = rbf(acc[mb][nb][r]);
+                        gate = rbf(acc[mb][nb + 2][r]);
+                    }
                     tp[ml * kTpStride + nb * 32 + l32] = (uint16_t)f2bf(rbf(gelu_tanh(gate)) * up);  // gemma4.py:197
                 }
         }
@@ -533,16 +615,20 @@ int pick_splits(int tiles, int ksteps, size_t rows_x_cols) {
     return sp;
 }
 
+template <FfnFormat F = FfnFormat::FP8>
 hipError_t gemm_partial(const GemmArgs& g, int splits, ScaleKind sk, hipStream_t s) {
     if (g.N % kCkBN || g.K % (kCkBK * splits) || (size_t)splits * g.M * g.N > kChunkPartFloats) return hipErrorInvalidValue;
     const dim3 grid(g.N / kCkBN, (g.M + kCkBM - 1) / kCkBM, splits);
+    if constexpr (F != FfnFormat::FP8) return ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32, F>, grid, s, g);
     return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32>, grid, s, g)
                                 : ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::BF16>, grid, s, g);
 }
 
+template <FfnFormat F = FfnFormat::FP8>
 hipError_t gemm_geglu(const GemmArgs& g, ScaleKind sk, hipStream_t s) {
     if (g.N % 64 || g.K % kCkBK) return hipErrorInvalidValue;
     const dim3 grid(g.N / 64, (g.M + kCkBM - 1) / kCkBM, 1);
+    if constexpr (F != FfnFormat::FP8) return ck_launch(chunk_gemm_kernel<Epi::GeGLU, ScaleKind::F32, F>, grid, s, g);
     return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<Epi::GeGLU, ScaleKind::F32>, grid, s, g)
                                 : ck_launch(chunk_gemm_kernel<Epi::GeGLU, ScaleKind::BF16>, grid, s, g);
 }
@@ -592,27 +678,36 @@ hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx
         : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.os, p.post_rms, res, nullptr, s);
 }
 
-hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
-    if (p.fmt != FfnFormat::FP8) return hipErrorInvalidValue;
+template <FfnFormat F>
+hipError_t ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
     uint16_t* res = p.residual + (size_t)m0 * kH;
     hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel<true>, dim3(M), s, (const uint16_t*)res, p.pre_rms, ctx->hbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
     g.x = ctx->hbuf; g.M = M; g.N = kL; g.K = kH;
     g.w[0] = p.up; g.w2 = p.gate; g.s0 = p.up_s; g.s2 = p.gate_s;
+    g.wsc[0] = (const uint8_t*)p.up_s; g.wsc2 = (const uint8_t*)p.gate_s; g.g0 = p.up_g; g.g2 = p.gate_g;
     g.y = ctx->pbuf;
-    e = gemm_geglu(g, p.scale_kind, s);
+    e = gemm_geglu<F>(g, p.scale_kind, s);
     if (e != hipSuccess) return e;
     GemmArgs d{};
     d.x = ctx->pbuf; d.M = M; d.N = kH; d.K = kL;
     d.w[0] = p.down; d.nseg[0] = 0; d.nseg[1] = kH; d.nsegs = 1;
+    d.wsc[0] = (const uint8_t*)p.down_s;
     d.yf = ctx->fbuf;
     const int sp = pick_splits(kH / kCkBN * m_tiles(M), kL / kCkBK, (size_t)M * kH);
-    e = gemm_partial(d, sp, p.scale_kind, s);
+    e = gemm_partial<F>(d, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
-    return p.scale_kind == ScaleKind::F32
-        ? post_rows<ScaleKind::F32>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s)
-        : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
+    return launch_ffn_post_rows(p, ctx->fbuf, sp, M, res, s);
+}
+
+hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    switch (p.fmt) {
+        case FfnFormat::FP8: return ffn_chunk<FfnFormat::FP8>(p, m0, M, s, ctx);
+        case FfnFormat::NVFP4: return ffn_chunk<FfnFormat::NVFP4>(p, m0, M, s, ctx);
+        case FfnFormat::MXFP4: return ffn_chunk<FfnFormat::MXFP4>(p, m0, M, s, ctx);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_qkv_heads(const QkvParams& p, int m0, int M, const float* part, int splits, hipStream_t s, DevCtx* ctx) {
@@ -638,13 +733,19 @@ hipError_t launch_ffn_post_rows(const FfnParams& p, const float* part, int split
             return p.scale_kind == ScaleKind::F32 ? post_rows<ScaleKind::F32>(part, splits, M, p.down_s, p.post_rms, res, p.layer_scalar, s)
                                                   : post_rows<ScaleKind::BF16>(part, splits, M, p.down_s, p.post_rms, res, p.layer_scalar, s);
         case FfnFormat::NVFP4:
-            if (splits > 4) return hipErrorInvalidValue;
-            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::NVFP4, 4>, dim3(M), s, part, splits, M,
-                             (const void*)nullptr, p.down_g, p.post_rms, res, p.layer_scalar);
+            if (splits > kCkSplitMax) return hipErrorInvalidValue;
+            return splits <= 4
+                ? ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::NVFP4, 4>, dim3(M), s, part, splits, M,
+                            (const void*)nullptr, p.down_g, p.post_rms, res, p.layer_scalar)
+                : ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::NVFP4>, dim3(M), s, part, splits, M,
+                            (const void*)nullptr, p.down_g, p.post_rms, res, p.layer_scalar);
         case FfnFormat::MXFP4:
-            if (splits > 4) return hipErrorInvalidValue;
-            return ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::MXFP4, 4>, dim3(M), s, part, splits, M,
-                             (const void*)nullptr, (const float*)nullptr, p.post_rms, res, p.layer_scalar);
+            if (splits > kCkSplitMax) return hipErrorInvalidValue;
+            return splits <= 4
+                ? ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::MXFP4, 4>, dim3(M), s, part, splits, M,
+                            (const void*)nullptr, (const float*)nullptr, p.post_rms, res, p.layer_scalar)
+                : ck_launch(chunk_post_rows_kernel<ScaleKind::F32, FfnFormat::MXFP4>, dim3(M), s, part, splits, M,
+                            (const void*)nullptr, (const float*)nullptr, p.post_rms, res, p.layer_scalar);
     }
     return hipErrorInvalidValue;
 }

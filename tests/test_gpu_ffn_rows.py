@@ -1,7 +1,7 @@
 """decoder_feedforward at 2..16 token rows: the matrix-core path (moa_rows.hip) that reads each
 weight once for all rows, in all three weight formats, vs the CPU oracle (which runs the
-reference's per-row algorithm, generate_references.py:375-414). Calls of more rows run in tiles of
-16 for the FP4 formats (a last tile of one row takes the single-row kernel). Each output row depends
+reference's per-row algorithm, generate_references.py:375-414). Calls of more rows take the MFMA
+path in every format. Each output row depends
 on its own input row only: the first rows of a call give the same bits as a call of just those
 rows."""
 import numpy as np
@@ -58,7 +58,8 @@ def test_rows_are_independent_and_repeatable(fmt):
 
 
 @pytest.mark.parametrize("fmt", ["nvfp4", "mxfp4"])
-def test_fp4_calls_of_17_rows_run_in_tiles(fmt):
+def test_fp4_calls_of_17_rows(fmt):
+    """17 rows: the first call length past the rows path (the MFMA path, a partial row tile)."""
     need_gpu()
     say(f"ffn rows {fmt} M17")
     want, got = FORMATS[fmt]

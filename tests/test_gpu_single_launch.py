@@ -1,6 +1,6 @@
 """The single-launch kernels (one token row) and the MFMA path of longer calls.
 
-Calls of more than 16 rows take the MFMA path (FP8 weights): 17 rows (a partial row tile),
+Calls of more than 16 rows take the MFMA path (every weight format): 17 rows (a partial row tile),
 64 (one full tile), 100 and 256 (BASELINE config 4's chunk length). Repeated calls interleaving
 different inputs check that no launch ever reads a tagged hand-off word left by an earlier launch
 (the tags are per-launch epochs): results must not depend on call history."""
@@ -9,7 +9,9 @@ import pytest
 
 from gpu_util import gate, gate_addend, need_gpu, say
 from moa_amd import synth
-from test_gpu_ffn import FFN_ATOL, gpu_fp8, oracle_fp8
+from test_gpu_ffn import (FFN_ATOL, assert_geglu_near_zero, cancel_fp4_codes, cancellation_residual, gpu_fp8,
+                          gpu_mxfp4, gpu_nvfp4, oracle_fp8, oracle_mxfp4, oracle_nvfp4)
+from oracle import oracle as O
 from test_gpu_o import run_gpu as o_gpu
 from test_gpu_o import run_oracle as o_oracle
 from test_gpu_qkv import check_against_oracle
@@ -24,6 +26,54 @@ def test_ffn_fp8_mfma_rows(M):
     say(f"ffn fp8 M{M} (MFMA path)")
     d = synth.cfg_ffn_fp8(5, M=M)
     gate(oracle_fp8(d), gpu_fp8(d), f"ffn fp8 M{M}", atol=FFN_ATOL)
+
+
+_fp4 = {}
+
+
+def fp4_case(fmt: str, M: int, tag: str = "mfma") -> dict:
+    if fmt not in _fp4:
+        _fp4[fmt] = synth.cfg_ffn_mxfp4(5) if fmt == "mxfp4" else synth.ref_ffn_inputs(5)
+    return dict(_fp4[fmt], residual=synth.bf16_normal(f"{tag}.{fmt}.M{M}.residual", (M, 3840)))
+
+
+@pytest.mark.parametrize("M", [17, 64, 256])
+@pytest.mark.parametrize("fmt", ["mxfp4", "nvfp4"])
+def test_ffn_fp4_mfma_rows(fmt, M):
+    """FP4 weights on the MFMA path: E2M1 codes widened with their block scales while they are
+    staged (weights read once per 256 rows)."""
+    need_gpu()
+    say(f"ffn {fmt} M{M} (MFMA path)")
+    d = fp4_case(fmt, M)
+    want, got = (oracle_mxfp4, gpu_mxfp4) if fmt == "mxfp4" else (oracle_nvfp4, gpu_nvfp4)
+    gate(want(d), got(d), f"ffn {fmt} M{M}", atol=FFN_ATOL)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "nvfp4", "fp8"])
+def test_ffn_mfma_rows_with_cancellation_probes(fmt):
+    """BASELINE config 3's cancellation probe at config 4's chunk length: rows 1 and 3 of 256 cancel
+    in every up/gate row (asserted near zero on the oracle), the rest are ordinary rows."""
+    need_gpu()
+    say(f"ffn {fmt} M256 with cancellation-probe rows (MFMA path)")
+    d = fp4_case(fmt, 256, "probe") if fmt != "fp8" else dict(synth.cfg_ffn_fp8(5, M=256))
+    d["residual"] = d["residual"].copy()
+    d["residual"][1] = cancellation_residual(-23)
+    d["residual"][3] = cancellation_residual(-12)
+    d["pre_ff_rms_weight"] = np.full(3840, 0x3F80, np.uint16)
+    for k in ("up", "gate"):
+        if fmt == "fp8":
+            w = d[f"{k}_weight"].copy()
+            w[:, 0::480] = 0x38
+            w[:, 1::480] = 0x38
+            d[f"{k}_weight"] = w
+        else:
+            d[f"{k}_weight_packed"] = cancel_fp4_codes(d[f"{k}_weight_packed"])
+    probes = dict(d, residual=np.ascontiguousarray(d["residual"][[1, 3]]))
+    assert_geglu_near_zero(probes, {"fp8": O.FFN_FP8, "mxfp4": O.FFN_MXFP4, "nvfp4": O.FFN_NVFP4}[fmt],
+                           f"ffn {fmt} M256 probes")
+    want, got = {"fp8": (oracle_fp8, gpu_fp8), "mxfp4": (oracle_mxfp4, gpu_mxfp4),
+                 "nvfp4": (oracle_nvfp4, gpu_nvfp4)}[fmt]
+    gate(want(d), got(d), f"ffn {fmt} M256 probes", atol=FFN_ATOL)
 
 
 def test_ffn_fp8_mfma_rows_without_post_norm_and_scalar():
