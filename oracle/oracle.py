@@ -8,13 +8,15 @@ All bf16 tensors are numpy uint16 arrays of raw bits; E4M3/E2M1/E8M0 are uint8 c
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# ORACLE_LIB names another build of the same source (tests/test_sanitizers.py: the ASan/UBSan one)
+LIB_PATH = Path(os.environ["ORACLE_LIB"]) if os.environ.get("ORACLE_LIB") else HERE / "liboracle.so"
 
 H, L, NS, GS, DS, QS, PS, TS, E, W = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768, 262144
 FFN_NVFP4, FFN_FP8, FFN_MXFP4 = 0, 1, 2
