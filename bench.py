@@ -101,7 +101,7 @@ def main() -> int:
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
                                           "ffn_mxfp4", "ffn_mxfp4_m16",
-                             "chunk"), default=None,
+                             "chunk", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     args = ap.parse_args()
@@ -327,6 +327,9 @@ def main() -> int:
         del g
         return float(np.median(per)), float(np.percentile(per, 10)), float(np.percentile(per, 90))
 
+    if args.profile == "floor":
+        floor_profile(torch, args.steps)
+        return 0
     if args.profile:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
@@ -543,6 +546,36 @@ def floor_measure(torch, np):
     log(f"attainable read rate {out['attainable_read_GBps']:.1f} GB/s ({out['attainable_shapes']})")
     del buf
     return out
+
+
+FLOOR_SEQUENCE = [  # (label, bytes, workgroups, threads) in dispatch order for --profile floor
+    ("empty o/ffn shape", 0, 240, 512), ("empty qkv shape", 0, 256, 576),
+    ("read o weights", WEIGHT_BYTES["o"], 240, 512), ("read qkv weights", WEIGHT_BYTES["qkv"], 256, 576),
+    ("read ffn weights", WEIGHT_BYTES["ffn"], 240, 512), ("read 1 GiB", 1 << 30, 1024, 512)]
+
+
+def floor_profile(torch, steps: int) -> None:
+    """Host-driven stream-read launches for a kernel trace: `steps` launches of each FLOOR_SEQUENCE
+    entry in order (reads rotated over a 1 GiB buffer, 1 GiB reads from a second one), with a
+    synchronisation between entries; then the 256 MiB copy of the other profiles."""
+    import ctypes as C
+
+    from moa_amd import _lib
+
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for label, nbytes, wg, thr in FLOOR_SEQUENCE:
+        for i in range(steps):
+            if nbytes == 1 << 30:
+                ptr = big.data_ptr()
+            else:
+                span = buf.numel() - nbytes
+                ptr = buf.data_ptr() + (((i * nbytes) % span) // 256 * 256 if nbytes else 0)
+            _lib.call("moa_bench_stream_read", C.c_void_p(ptr), C.c_uint64(nbytes), wg, thr, C.c_void_p(sink.data_ptr()), st)
+        torch.cuda.synchronize()
+        log(f"profile floor: {steps} x {label} ({nbytes} B, {wg} x {thr})")
 
 
 LOGITS_CPU_ROWS = 16384  # vocabulary rows of the CPU logits sample (1/16 of the vocabulary)
