@@ -135,8 +135,11 @@ constexpr int kCkNt = 2;  // cache policy: non-temporal (weights are read once)
 //   All loads are buffer loads whose per-lane offsets are fixed: the step moves the scalar
 //   offset only. Prefetches past the last step repeat the last step (harmless), so the loop body
 //   has no branches.
-template <Epi E, ScaleKind SK, FfnFormat F = FfnFormat::FP8>
+template <Epi E, ScaleKind SK, FfnFormat F = FfnFormat::FP8, int BN = kCkBN>
 __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) void chunk_gemm_kernel(GemmArgs g) {
+    static_assert(BN == 128 || (BN == 64 && E == Epi::F32Partial), "128 weight rows, or 64 for split-K partials");
+    constexpr int NB = BN / 32;   // 32-column blocks per wave
+    constexpr int RPT = BN / 64;  // staged weight rows per thread
     constexpr bool FP4 = F != FfnFormat::FP8;
     // bytes per weight row and per 64-k step; FP4 block-scale bytes per row and per step
     const int rb = FP4 ? g.K / 2 : g.K;
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int sb = F == FfnFormat::NVFP4 ? g.K / 16 : (F == FfnFormat::MXFP4 ? g.K / 32 : 0);
     constexpr int kStepS = F == FfnFormat::NVFP4 ? 4 : 2;
     // three weight buffers during the loop; the GeGLU epilogue reuses the space for its transpose
-    constexpr int kWsBytes = kCkBN * kCkWStride, kTpStride = 72;
+    constexpr int kWsBytes = BN * kCkWStride, kTpStride = 72;
     constexpr int kLds = 3 * kWsBytes > 4 * 64 * kTpStride * 2 ? 3 * kWsBytes : 4 * 64 * kTpStride * 2;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kLds];
     uint8_t(*ws)[kWsBytes] = reinterpret_cast<uint8_t(*)[kWsBytes]>(smem);
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int m_wave = m_blk + wave * 64;
     const int kz = g.K / gridDim.z, kbeg = blockIdx.z * kz, nsteps = kz / kCkBK;
 
-    // staged weight rows of this thread: tile rows r0 and r0 + 64, k 16 q .. 16 q + 15 of each step
+    // staged weight rows of this thread: tile row r0 (and r0 + 64 when BN = 128), k 16 q .. 16 q + 15 of each step
     // (FP8: 16 bytes; FP4: 8 bytes of codes and the one block-scale code covering them)
     const int r0 = t >> 2, q = t & 3;
     __amdgpu_buffer_rsrc_t wrs[2], srs[2];
@@ -174,13 +177,13 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
             svo[0] = svo[1] = r0 * sb + scol;
         }
     } else {
-        const int n0 = blockIdx.x * kCkBN;
+        const int n0 = blockIdx.x * BN;
         while (seg + 1 < g.nsegs && n0 >= g.nseg[seg + 1]) ++seg;
-        wrs[0] = wrs[1] = ck_rsrc(g.w[seg] + (size_t)(n0 - g.nseg[seg]) * rb, (uint32_t)kCkBN * rb);
+        wrs[0] = wrs[1] = ck_rsrc(g.w[seg] + (size_t)(n0 - g.nseg[seg]) * rb, (uint32_t)BN * rb);
         wvo[0] = r0 * rb + kcol;
         wvo[1] = (r0 + 64) * rb + kcol;
         if constexpr (FP4) {
-            srs[0] = srs[1] = ck_rsrc(g.wsc[seg] + (size_t)(n0 - g.nseg[seg]) * sb, (uint32_t)kCkBN * sb);
+            srs[0] = srs[1] = ck_rsrc(g.wsc[seg] + (size_t)(n0 - g.nseg[seg]) * sb, (uint32_t)BN * sb);
             svo[0] = r0 * sb + scol;
             svo[1] = (r0 + 64) * sb + scol;
         }
@@ -194,11 +197,11 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) avo[mb] = ((wave * 2 + mb) * kst * 2048 + lane * 8) * 2 + (kbeg / kCkBK) * 4096;
 
-    f32x16 acc[2][4];
+    f32x16 acc[2][NB];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
@@ -212,20 +215,21 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         const int so = min(s, last) * kStepB;
         if constexpr (FP4) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < RPT; ++i) {
                 const auto v = __builtin_amdgcn_raw_buffer_load_b64(wrs[i], wvo[i], so, kCkNt);
                 dst[i].x = v[0];
                 dst[i].y = v[1];
                 dst[i].z = __builtin_amdgcn_raw_buffer_load_b8(srs[i], svo[i], min(s, last) * kStepS, 0);
             }
         } else {
-            dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[0], wvo[0], so, kCkNt));
-            dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[1], wvo[1], so, kCkNt));
+#pragma unroll
+            for (int i = 0; i < RPT; ++i)
+                dst[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wrs[i], wvo[i], so, kCkNt));
         }
     };
     auto store_w = [&](const uint4 (&src)[2], int buf) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < RPT; ++i) {
             bf16x8* d = reinterpret_cast<bf16x8*>(&ws[buf][i ? wdst1 : wdst0]);
             if constexpr (FP4) {
                 d[0] = fp4x8_to_bf16<F>(src[i].x, src[i].z);
@@ -249,8 +253,8 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int j = 0; j < 4; ++j) dst[j] = bp[j];
     };
-    auto mfma8 = [&](const uint4 (&a)[2][4], const bf16x8 (&b)[4], auto NB) {
-        constexpr int nb = decltype(NB)::value;
+    auto mfma8 = [&](const uint4 (&a)[2][4], const bf16x8 (&b)[4], auto NBI) {
+        constexpr int nb = decltype(NBI)::value;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     load_w(wr[1], WD + 1);
     __syncthreads();
     read_b(bb[0], 0, 0);
-    auto body = [&](auto P, int s) {
+    auto body4 = [&](auto P, int s) {
         constexpr int c = decltype(P)::value;  // s mod 6
         constexpr int cb = c % 3, nbuf = (c + 1) % 3;
         const uint4(&a)[2][4] = ar[c % 3];
@@ -341,6 +345,58 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
+    // BN = 64: two fragments per step. Fragment 0 carries the staging (widenings and LDS writes of
+    // W(s + 2)) beside fragment 1's LDS reads; fragment 1 the A and weight prefetches and, last of
+    // the step's LDS operations, the next step's first fragment -- so lgkmcnt(4) at the barrier
+    // still leaves every LDS write of this wave complete.
+    auto body2 = [&](auto P, int s) {
+        constexpr int c = decltype(P)::value;  // s mod 6
+        constexpr int cb = c % 3, nbuf = (c + 1) % 3;
+        const uint4(&a)[2][4] = ar[c % 3];
+        constexpr int kDsR = 0x100, kDsW = 0x200, kVmR = 0x020, kValu = 0x002, kMfma = 0x008;
+        constexpr int kWLoads = FP4 ? 2 : 1;
+        constexpr int kWValu = F == FfnFormat::NVFP4 ? 4 : 1;
+        read_b(bb[1], cb, 1);
+        store_w(wr[(c + 2) % WD], (c + 2) % 3);
+        mfma8(a, bb[0], Par<0>{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kDsR, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kValu, kWValu, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kValu, kWValu, 0);
+            __builtin_amdgcn_sched_group_barrier(kDsW, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(ar[(c + 2) % 3], s + 2);
+        load_w(wr[(c + 2) % WD], s + 2 + WD);
+        read_b(bb[0], nbuf, 0);
+        mfma8(a, bb[1], Par<1>{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kVmR, 2, 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(kDsR, 1, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(kVmR, kWLoads, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        __asm__ volatile("s_waitcnt lgkmcnt(4)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto body = [&](auto P, int s) {
+        if constexpr (NB == 4) body4(P, s);
+        else body2(P, s);
+    };
     int s = 0;
     for (; s + 5 < nsteps; s += 6) {
         body(Par<0>{}, s);
@@ -363,9 +419,9 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     // per-element tests (a test per element would serialise the 64-128 element computations).
     const bool full = m_wave + 64 <= g.M;
     if constexpr (E == Epi::F32Partial) {
-        float* yz = g.yf + (size_t)blockIdx.z * g.M * g.N + blockIdx.x * kCkBN + l32;
+        float* yz = g.yf + (size_t)blockIdx.z * g.M * g.N + blockIdx.x * BN + l32;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -452,7 +508,7 @@ __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint
     uint32_t h[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
+        h[i] = pk_bf16((xv[2 * i] * inv) * wv[2 * i], (xv[2 * i + 1] * inv) * wv[2 * i + 1]);
     const size_t o0 = Tiles ? atile_off(m, c * 16, kH) : (size_t)m * kH + c * 16;
     const size_t o1 = Tiles ? atile_off(m, c * 16 + 8, kH) : (size_t)m * kH + c * 16 + 8;
     *reinterpret_cast<uint4*>(out + o0) = make_uint4(h[0], h[1], h[2], h[3]);
@@ -615,13 +671,20 @@ int pick_splits(int tiles, int ksteps, size_t rows_x_cols) {
     return sp;
 }
 
-template <FfnFormat F = FfnFormat::FP8>
+// Weight rows per workgroup of a split-K projection. The O projection (K = 4096) takes 64: twice
+// the tiles of 128-row tiles, so half the k splits fill the device and half the f32 partial sums
+// are written and read back (measured at M = 256: GEMM 17.3 -> 16.5 us, post rows 9.1 -> 6.9 us).
+// QKV and down keep 128, whose main loop does twice the MFMA work per A load and per barrier
+// (with 64, down measured 39.1 -> 44.6 us against 9.5 -> 7.1 us saved in its post rows).
+constexpr int kCkOBN = 64;
+
+template <FfnFormat F = FfnFormat::FP8, int BN = kCkBN>
 hipError_t gemm_partial(const GemmArgs& g, int splits, ScaleKind sk, hipStream_t s) {
-    if (g.N % kCkBN || g.K % (kCkBK * splits) || (size_t)splits * g.M * g.N > kChunkPartFloats) return hipErrorInvalidValue;
-    const dim3 grid(g.N / kCkBN, (g.M + kCkBM - 1) / kCkBM, splits);
-    if constexpr (F != FfnFormat::FP8) return ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32, F>, grid, s, g);
-    return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32>, grid, s, g)
-                                : ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::BF16>, grid, s, g);
+    if (g.N % BN || g.K % (kCkBK * splits) || (size_t)splits * g.M * g.N > kChunkPartFloats) return hipErrorInvalidValue;
+    const dim3 grid(g.N / BN, (g.M + kCkBM - 1) / kCkBM, splits);
+    if constexpr (F != FfnFormat::FP8) return ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32, F, BN>, grid, s, g);
+    return sk == ScaleKind::F32 ? ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::F32, F, BN>, grid, s, g)
+                                : ck_launch(chunk_gemm_kernel<Epi::F32Partial, ScaleKind::BF16, F, BN>, grid, s, g);
 }
 
 template <FfnFormat F = FfnFormat::FP8>
@@ -657,9 +720,15 @@ hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, De
     const int sp = pick_splits(kQkvRowsTotal / kCkBN * m_tiles(M), kH / kCkBK, (size_t)M * kQkvRowsTotal);
     e = gemm_partial(g, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
+    if (sp <= 2) return launch_qkv_heads(p, m0, M, ctx->fbuf, sp, s, ctx);
+    const float* part = ctx->fbuf;
+    if (sp <= 4)  // as many partial loads in flight as there are splits
+        return p.scale_kind == ScaleKind::F32
+            ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32, 4>, dim3(32, M), s, p, m0, M, part, sp, ctx->err)
+            : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16, 4>, dim3(32, M), s, p, m0, M, part, sp, ctx->err);
     return p.scale_kind == ScaleKind::F32
-        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32>, dim3(32, M), s, p, m0, M, (const float*)ctx->fbuf, sp, ctx->err)
-        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16>, dim3(32, M), s, p, m0, M, (const float*)ctx->fbuf, sp, ctx->err);
+        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32>, dim3(32, M), s, p, m0, M, part, sp, ctx->err)
+        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16>, dim3(32, M), s, p, m0, M, part, sp, ctx->err);
 }
 
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
@@ -669,8 +738,8 @@ hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx
     g.x = ctx->pbuf; g.M = M; g.N = kH; g.K = kQs;
     g.w[0] = p.ow; g.nseg[0] = 0; g.nseg[1] = kH; g.nsegs = 1;
     g.yf = ctx->fbuf;
-    const int sp = pick_splits(kH / kCkBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
-    e = gemm_partial(g, sp, p.scale_kind, s);
+    const int sp = pick_splits(kH / kCkOBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
+    e = gemm_partial<FfnFormat::FP8, kCkOBN>(g, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
     uint16_t* res = p.residual + (size_t)m0 * kH;
     return p.scale_kind == ScaleKind::F32
