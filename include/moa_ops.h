@@ -221,8 +221,8 @@ int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* 
                               int M, int N, int K, void* stream);
 
 /* Test support: decodes every E4M3 code, E2M1 byte, E8M0 code, bf16 GeLU input and bf16
- * final-logit softcap input with the kernels' own device helpers into out (device uint32
- * [132100]; layout in moa_decode.hip). */
+ * final-logit softcap input, and rounds f32 values of every bf16 high half to bf16, with the
+ * kernels' own device helpers into out (device uint32 [721924]; layout in moa_decode.hip). */
 int moa_format_selftest(uint32_t* out, void* stream);
 
 /* Test support for the launch epochs of the one-token kernels (no counterpart in the reference).

@@ -261,7 +261,7 @@ __device__ __forceinline__ void rms_finish_bf16(const RmsStage& s, uint16_t* __r
         uint32_t h[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
+            h[i] = pk_bf16((xv[2 * i] * inv) * wv[2 * i], (xv[2 * i + 1] * inv) * wv[2 * i + 1]);
         *reinterpret_cast<uint4*>(lds + t * 16) = make_uint4(h[0], h[1], h[2], h[3]);
         *reinterpret_cast<uint4*>(lds + t * 16 + 8) = make_uint4(h[4], h[5], h[6], h[7]);
     }
@@ -307,7 +307,7 @@ __device__ __forceinline__ void wave_rms_finish(const WaveRms& s, uint16_t* __re
             uint32_t h[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                h[e] = f2bf((v[2 * e] * inv) * wv[2 * e]) | (f2bf((v[2 * e + 1] * inv) * wv[2 * e + 1]) << 16);
+                h[e] = pk_bf16((v[2 * e] * inv) * wv[2 * e], (v[2 * e + 1] * inv) * wv[2 * e + 1]);
             *reinterpret_cast<uint4*>(lds + c * 8) = make_uint4(h[0], h[1], h[2], h[3]);
         }
     }
@@ -846,7 +846,7 @@ __device__ __forceinline__ uint4 o_input_chunk(uint4 v, const float* div, int k)
     uint32_t h[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        h[i] = f2bf(d > 0.0f ? f[2 * i] / d : 0.0f) | (f2bf(d > 0.0f ? f[2 * i + 1] / d : 0.0f) << 16);
+        h[i] = pk_bf16(d > 0.0f ? f[2 * i] / d : 0.0f, d > 0.0f ? f[2 * i + 1] / d : 0.0f);
     return make_uint4(h[0], h[1], h[2], h[3]);
 }
 
@@ -1230,7 +1230,7 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         // first read of p; words not yet current are read again until they are.
         if (ctl && lane < kFfnWaves * kUgRL / 2)
             publish64(ptag + blockIdx.x * (kFfnWaves * kUgRL / 2) + lane,
-                      tagged(tag, f2bf(pl[2 * lane]) | (f2bf(pl[2 * lane + 1]) << 16)));
+                      tagged(tag, pk_bf16(pl[2 * lane], pl[2 * lane + 1])));
         __syncthreads();  // the publish is issued ahead of every load below
         constexpr int PW = kL / 2 / kFfnBlock;  // 15 words per thread
         static_assert(PW * kFfnBlock == kL / 2, "p words per thread");
@@ -1368,6 +1368,13 @@ __global__ void format_selftest_kernel(uint32_t* out) {
     if (i < 65536) {
         out[1024 + i] = f2bf(gelu_tanh(bf2f((uint32_t)i)));
         out[66564 + i] = softcap30_bf16(bf2f((uint32_t)i));
+        // f32 -> bf16 rounding: every bf16 high half with eight low halves (zero, one, below, at and
+        // above the tie, ...), then one packed pair per high half
+        const uint32_t lows[8] = {0x0000u, 0x0001u, 0x7fffu, 0x8000u, 0x8001u, 0x4000u, 0xc000u, 0xffffu};
+        const uint32_t hi = (uint32_t)i << 16;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[132100 + 8 * i + j] = f2bf(__uint_as_float(hi | lows[j]));
+        out[656388 + i] = pk_bf16(__uint_as_float(hi | 0x8000u), __uint_as_float(hi | 0x7fffu));
     }
 }
 

@@ -23,10 +23,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // ------------------------------------------------------------------ bf16
 __device__ __forceinline__ float bf2f(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
-__device__ __forceinline__ uint32_t f2bf(float v) {
-    uint32_t b = __float_as_uint(v);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-    return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+// f32 -> bf16 bits, round half to even: one v_cvt_pk_bf16_f32. For every non-NaN f32 it gives
+// the bits of rounding the raw f32 bits, (b + 0x7fff + lsb) >> 16 (fixture_prng.py:80-90; the
+// format self-test checks every bf16 high half with ties, near-ties and subnormals); a NaN
+// stays a (quiet) NaN.
+__device__ __forceinline__ uint32_t f2bf(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+
+// Two f32 to packed bf16 (lo in the low half), rounded as f2bf: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2_t));
 }
 
 // Round an f32 through bf16 and back (the per-op bf16 commit of a torch bf16 tensor op).

@@ -404,7 +404,7 @@ __global__ __launch_bounds__(kFaBlock) void fattn_combine_kernel(const float* __
             o1 = fmaf(f, oc[c].y, o1);
         }
     }
-    *op = f2bf(o0) | (f2bf(o1) << 16);
+    *op = pk_bf16(o0, o1);
     if (t == 0) {
         rmax[sh] = mn;
         rsum[sh] = l;
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(kFaBlock) void fattn_merge_kernel(const float* __re
         sl += wl[k];
     }
     const size_t sh = (size_t)m * kGf + h;
-    *reinterpret_cast<uint32_t*>(out + sh * kDf + d) = f2bf(s0) | (f2bf(s1) << 16);
+    *reinterpret_cast<uint32_t*>(out + sh * kDf + d) = pk_bf16(s0, s1);
     if (db == 0 && dp == 0) {
         rmax[sh] = mx;
         rsum[sh] = sl;

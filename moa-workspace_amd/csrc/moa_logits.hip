@@ -65,7 +65,7 @@ __global__ __launch_bounds__(kLgBlock) void logits_kernel(const uint16_t* __rest
             uint32_t h[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                h[i] = f2bf((xv[2 * i] * inv) * wv[2 * i]) | (f2bf((xv[2 * i + 1] * inv) * wv[2 * i + 1]) << 16);
+                h[i] = pk_bf16((xv[2 * i] * inv) * wv[2 * i], (xv[2 * i + 1] * inv) * wv[2 * i + 1]);
             *reinterpret_cast<uint4*>(&xs[m][c * 16]) = make_uint4(h[0], h[1], h[2], h[3]);
             *reinterpret_cast<uint4*>(&xs[m][c * 16 + 8]) = make_uint4(h[4], h[5], h[6], h[7]);
         }

@@ -220,7 +220,7 @@ __device__ __forceinline__ void rw_rows_load(RwRows<NT, KR>& st, const uint16_t*
                 uint32_t h[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    h[e] = f2bf(d > 0.0f ? f[2 * e] / d : 0.0f) | (f2bf(d > 0.0f ? f[2 * e + 1] / d : 0.0f) << 16);
+                    h[e] = pk_bf16(d > 0.0f ? f[2 * e] / d : 0.0f, d > 0.0f ? f[2 * e + 1] / d : 0.0f);
                 st.v[i] = make_uint4(h[0], h[1], h[2], h[3]);
             }
         }

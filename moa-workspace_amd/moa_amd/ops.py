@@ -256,7 +256,7 @@ def device_errors(device: torch.device | None = None) -> int:
 
 
 def format_selftest(device="cuda") -> torch.Tensor:
-    out = torch.zeros(132100, dtype=torch.int32, device=device)  # layout: moa_decode.hip format_selftest_kernel
+    out = torch.zeros(721924, dtype=torch.int32, device=device)  # layout: moa_decode.hip format_selftest_kernel
     _lib.call("moa_format_selftest", C.c_void_p(out.data_ptr()), _stream(out))
     return out
 

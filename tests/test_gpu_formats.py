@@ -41,3 +41,30 @@ def test_device_decoders_and_gelu_exhaustive():
     assert mism.sum() <= 64
     d = np.abs(prng.bf16_bits_to_f32(got[mism]) - prng.bf16_bits_to_f32(ref[mism]))
     assert np.all(d <= np.maximum(np.abs(prng.bf16_bits_to_f32(ref[mism])) * 2.0 ** -7, 2.0 ** -20))
+
+
+def test_device_bf16_rounding():
+    """The kernels' f32 -> bf16 rounding (v_cvt_pk_bf16_f32) against the raw-bit rule of
+    fixture_prng.py:80-90 (prng.f32_to_bf16_bits): every bf16 high half with eight low halves --
+    zero, one, just below, at and just above the tie, a quarter, three quarters, all ones -- so
+    ties to even, carries into the exponent, subnormals, overflow to infinity and NaN inputs are
+    all covered; plus the packed pair helper on every high half."""
+    need_gpu()
+    from moa_amd import ops
+    say("format selftest: f32 -> bf16 rounding x524288, packed pairs x65536")
+    out = host(ops.format_selftest()).view(np.uint32)
+    hi = np.arange(1 << 16, dtype=np.uint32) << np.uint32(16)
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0x4000, 0xC000, 0xFFFF], np.uint32)
+    src = (hi[:, None] | lows[None, :]).reshape(-1)
+    want = prng.f32_to_bf16_bits(src.view(np.float32))
+    got = out[132100:132100 + src.size].astype(np.uint16)
+    nan_in = np.isnan(src.view(np.float32))
+    assert np.all(np.isnan(prng.bf16_bits_to_f32(got[nan_in]))), "a NaN input lost its NaN"
+    bad = ~nan_in & (got != want)
+    assert not bad.any(), f"{int(bad.sum())} roundings differ, first input {src[bad][0]:#010x}"
+    pair = out[656388:656388 + (1 << 16)]
+    lo_src, hi_src = (hi | np.uint32(0x8000)).view(np.float32), (hi | np.uint32(0x7FFF)).view(np.float32)
+    want_lo, want_hi = prng.f32_to_bf16_bits(lo_src), prng.f32_to_bf16_bits(hi_src)
+    fin = ~np.isnan(lo_src)
+    assert np.array_equal((pair & 0xFFFF)[fin].astype(np.uint16), want_lo[fin])
+    assert np.array_equal((pair >> 16)[fin].astype(np.uint16), want_hi[fin])
