@@ -240,6 +240,19 @@ int moa_test_epoch_tag(int kernel, uint64_t old, uint32_t* tag);
  * billions of launches. Synchronous; no call may be in flight on the device. */
 int moa_test_preset_epochs(uint64_t launches);
 
+/* Test support for the waits of the one-token QKV, O and FFN kernels (no counterpart in the
+ * reference). A workgroup that has waited steal_ticks (100 MHz wall-clock ticks; 50000 by
+ * default) for another workgroup of its launch computes that workgroup's share itself, so a call
+ * completes with the same bits whether or not its whole grid is resident. With hold_ticks > 0,
+ * workgroups hold[0..3] (-1: none) of every later launch wait hold_ticks at entry, before they read
+ * or write anything -- as if they had been started late. Applies to calls issued after it;
+ * steal_ticks 0 restores the defaults (no hold). */
+int moa_test_set_stall(uint32_t steal_ticks, uint32_t hold_ticks, const int32_t* hold);
+
+/* Test support: the number of take-overs (a wait that did another workgroup's share) on the
+ * current device since the last call, then resets it. Synchronises the device. */
+int moa_test_take_overs(uint32_t* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -556,6 +556,31 @@ int moa_test_preset_epochs(uint64_t launches) {
     return finish(e, "presetting the epoch counters");
 }
 
+int moa_test_set_stall(uint32_t steal_ticks, uint32_t hold_ticks, const int32_t* hold) {
+    Stall st = {kStealTicks, 0, {-1, -1, -1, -1}};
+    if (steal_ticks) {
+        st.steal_ticks = steal_ticks;
+        st.hold_ticks = hold ? hold_ticks : 0;
+        for (int i = 0; i < 4 && hold; ++i) st.hold[i] = hold[i];
+    }
+    set_stall(st);
+    return MOA_SUCCESS;
+}
+
+int moa_test_take_overs(uint32_t* count) {
+    Check c;
+    c.ptr(count, "count", 1);
+    if (c.code) return c.code;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(count, ctx->err + kErrTakeOvers, sizeof(uint32_t), hipMemcpyDeviceToHost);
+    const uint32_t zero = 0;
+    if (e == hipSuccess) e = hipMemcpy(ctx->err + kErrTakeOvers, &zero, sizeof zero, hipMemcpyHostToDevice);
+    return finish(e, "reading the take-over count");
+}
+
 int moa_format_selftest(uint32_t* out, void* stream) {
     Check c;
     c.ptr(out, "out", 4);

@@ -78,10 +78,13 @@ __device__ __forceinline__ bool block_arrive_tree(uint32_t* tree, uint32_t nbloc
 }
 
 // Post-norm hand-off of the single-launch O and FFN kernels (240 workgroups of 16 output rows):
-// per workgroup one partial sum of squares (f32 bits) and eight words of two bf16 outputs.
+// per workgroup one partial sum of squares (f32 bits) and eight words of two bf16 outputs; the FFN
+// also keeps per workgroup the tag of the last launch whose up/gate rows of that block have been
+// claimed (claim words are exchanged, never polled).
 struct PostSlots {
     uint64_t part[kFfnPartSlots];
     uint64_t d[kFfnPartSlots][8];
+    uint64_t claim[kFfnPartSlots];
 };
 static_assert(sizeof(PostSlots) == sizeof(uint64_t) * kFfnSlotWords, "slot area size");
 constexpr int kPostGrid = 240;     // workgroups of a post-norm hand-off
@@ -89,6 +92,16 @@ constexpr int kPostWgRows = 16;    // output rows per workgroup
 constexpr int kPostLeaders = 8;    // leader workgroups
 constexpr int kPostGroup = kPostGrid / kPostLeaders;  // 30 workgroups per leader
 static_assert(kPostGrid * kPostWgRows == kH && 2 * kPostGroup <= 64, "a leader lane owns 8 outputs");
+
+// Test only (Stall::hold; the kernels' Hold instantiations, launched only while a test holds
+// workgroups): the held workgroups of a launch wait at entry, bounded by the wall clock.
+__device__ __forceinline__ void stall_hold(const Stall& st) {
+    if (st.hold_ticks == 0) return;
+    const int b = blockIdx.x;
+    if (b != st.hold[0] && b != st.hold[1] && b != st.hold[2] && b != st.hold[3]) return;
+    const uint64_t t0 = wall_clock64();
+    while (wall_clock64() - t0 < st.hold_ticks) __builtin_amdgcn_s_sleep(64);
+}
 
 // One wave of every workgroup b: publish its 16 outputs (bf16 bits dl[0..16)) and its partial sum
 // of squares (in row order).
@@ -103,6 +116,20 @@ __device__ __forceinline__ void post_publish(PostSlots* slots, uint32_t tag, con
     }
 }
 
+// post_publish for workgroup b from registers (lane i < 16 holds output i): the same words and the
+// same partial sum, for a wave that computed another workgroup's outputs.
+__device__ __forceinline__ void post_publish_vals(PostSlots* slots, uint32_t tag, int b, uint32_t v, int lane) {
+    const uint32_t lo = __shfl(v, (2 * lane) & 15, kWave), hi = __shfl(v, (2 * lane + 1) & 15, kWave);
+    if (lane < kPostWgRows / 2) publish64(&slots->d[b][lane], tagged(tag, lo | (hi << 16)));
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPostWgRows; ++i) {
+        const float f = bf2f(__shfl(v, i, kWave));
+        ss = fmaf(f, f, ss);
+    }
+    if (lane == 0) publish64(&slots->part[b], tagged(tag, __float_as_uint(ss)));
+}
+
 // Rows owned by lane l of leader g: 8 outputs of workgroup g + 8 (l / 2), from row (l % 2) * 8.
 __device__ __forceinline__ int post_leader_row(int lane) {
     return (blockIdx.x + kPostLeaders * min(lane / 2, kPostGroup - 1)) * kPostWgRows + (lane % 2) * 8;
@@ -111,12 +138,16 @@ __device__ __forceinline__ int post_leader_row(int lane) {
 // One wave of leader workgroup g < kPostLeaders: poll until all 240 partial sums and the outputs of
 // workgroups g, g + 8, ... carry `tag`; sum the partials in a fixed order (the same bits in every
 // leader) and write those workgroups' residual rows in place (nothing when the poll expired, so
-// rows are never computed from stale words):
+// rows are never computed from stale words). After steal_ticks of waiting the wave computes and
+// publishes the lowest missing workgroup's outputs itself (steal(b): the same bits as workgroup b's
+// own), then polls again at once:
 //   out = bf16(bf16(r + bf16(bf16(d * inv) * w)) * ls)    (ls skipped when has_ls is false)
 // FO/src/device/shared/rmsnorm.rs:204-296 + residual.rs:189-241. r8 / w8: the lane's residual and
 // norm-weight values (prefetched by the caller at post_leader_row).
+template <typename Steal>
 __device__ __forceinline__ void post_leader(PostSlots* slots, uint32_t tag, uint16_t* res, const uint4& r8,
-                                            const uint4& w8, bool has_ls, float lsv, int lane, uint32_t* err) {
+                                            const uint4& w8, bool has_ls, float lsv, int lane, uint32_t* err,
+                                            uint32_t steal_ticks, Steal steal) {
     constexpr int NP = (kPostGrid + 63) / 64;
     float part[NP];
     uint32_t dq[4];
@@ -126,24 +157,40 @@ __device__ __forceinline__ void post_leader(PostSlots* slots, uint32_t tag, uint
     bool expired = false;
     for (;;) {
         bool ok = true;
+        int victim = kPostGrid;  // the lowest workgroup with a stale word (uniform)
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             const bool real = lane + 64 * i < kPostGrid;
             const uint64_t v = collect64(&slots->part[min(lane + 64 * i, kPostGrid - 1)]);
             part[i] = real ? __uint_as_float((uint32_t)v) : 0.0f;
-            ok = ok && (!real || (uint32_t)(v >> 32) == tag);
+            const bool stale = real && (uint32_t)(v >> 32) != tag;
+            ok = ok && !stale;
+            const uint64_t m = __ballot(stale);
+            if (m && victim == kPostGrid) victim = 64 * i + __builtin_ctzll(m);
         }
+        bool dstale = false;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint64_t v = collect64(&slots->d[lwg][(lane % 2) * 4 + k]);
             dq[k] = (uint32_t)v;
-            ok = ok && (!mine_rows || (uint32_t)(v >> 32) == tag);
+            dstale = dstale || (mine_rows && (uint32_t)(v >> 32) != tag);
         }
+        ok = ok && !dstale;
         if (__all(ok)) break;
-        if (wall_clock64() - t0 > kSpinTicks) {
+        const uint64_t dt = wall_clock64() - t0;
+        if (dt > kSpinTicks) {
             if (lane == 0) atomicOr(err, kErrSpinTimeout);
             expired = true;
             break;
+        }
+        if (__builtin_expect(dt > steal_ticks, 0)) {
+            const uint64_t md = __ballot(dstale);
+            if (victim == kPostGrid && md) victim = blockIdx.x + kPostLeaders * (__builtin_ctzll(md) / 2);
+            if (victim < kPostGrid) {
+                if (lane == 0) atomicAdd(err + kErrTakeOvers, 1u);
+                steal(victim);
+                continue;
+            }
         }
         __builtin_amdgcn_s_sleep(1);
     }
@@ -668,6 +715,10 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
 // epoch (the head's epoch counter gets one add per workgroup at entry; epoch_tag) and polls the
 // head's 8 tagged words. Then the
 // control wave normalises, rotates and stores the workgroup's 32 values.
+// Every output depends only on the inputs (nothing is read that the launch writes), so a control
+// wave that has waited stall.steal_ticks for a sibling's partial sum computes that sibling's 32 rows
+// itself, publishes their partial sum and stores their outputs too; a sibling that was only late
+// writes the same bits again.
 constexpr int kQkvWaves = 8;                                // row waves; wave 8 is the control wave
 constexpr int kQkvBlock = 64 * (kQkvWaves + 1);
 constexpr int kQkvRowsW = 4;                                // rows per row wave
@@ -681,11 +732,13 @@ static_assert(32 * kQkvPerHead == kQkvSlotWords, "one tagged word per workgroup"
 // Head-local row of slot s = 4 w + r (w < 4: first half of the head, w >= 4: second half).
 __device__ __forceinline__ int qkv_local_row(int q, int s) { return s < 16 ? 16 * q + s : 128 + 16 * q + (s - 16); }
 
-template <ScaleKind SK>
+template <ScaleKind SK, bool Hold = false>
 __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m0, uint64_t* slots, uint32_t* tickets,
-                                                              uint32_t* err) {
+                                                              uint32_t* err, Stall stall) {
     __shared__ uint16_t hs[kH];
     __shared__ float raw[kQkvWgRows];
+    __shared__ float sraw[kQkvPerHead][kQkvWgRows];  // rows of siblings taken over
+    if constexpr (Hold) stall_hold(stall);
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kQkvWaves;
     const int head = blockIdx.x / kQkvPerHead, q = blockIdx.x % kQkvPerHead;
@@ -697,7 +750,8 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
     if (head < 16) { W = p.qw; S = p.qs; }
     else if (head < 24) { W = p.kw; S = p.ks; }
     else { W = p.vw; S = p.vs; }
-    const int mrow0 = (head < 16 ? head : (head < 24 ? head - 16 : head - 24)) * kDs + t0;  // row in its matrix
+    const int hrow0 = (head < 16 ? head : (head < 24 ? head - 16 : head - 24)) * kDs;  // the head's first row in its matrix
+    const int mrow0 = hrow0 + t0;
     const float scale = load_scale<SK>(S, mrow0 + min(lane, kQkvRowsW - 1));
 
     // Control wave: offsets and norm weight at entry (ahead of every weight load, so waiting for
@@ -788,15 +842,71 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
         for (int i = 0; i < kQkvWgRows; ++i) ss = fmaf(raw[i], raw[i], ss);  // exact squares of bf16
         publish64(hslots + q, tagged(tag, __float_as_uint(ss)));
     }
-    float part = 0.0f;
+    // sibling qv's 32 raw rows by this wave, each row as qv's row waves compute it, into sraw[qv];
+    // then their partial sum, published as qv would, and returned
+    auto take_over = [&](int qv) -> float {
+        float rv = 0.0f;  // lane s < 32: slot s
+#pragma unroll 1
+        for (int w = 0; w < kQkvWaves; ++w) {
+            const int row = hrow0 + qkv_local_row(qv, w * kQkvRowsW);
+            uint4 sq[kQkvRowsW][KI];
+#pragma unroll
+            for (int r = 0; r < kQkvRowsW; ++r)
+#pragma unroll
+                for (int j = 0; j < KI; ++j) {
+                    const int col = j * 1024 + lane * 16;
+                    const uint4 v = ld_stream(W + (size_t)(row + r) * kH + (col < kH ? col : 0));
+                    sq[r][j] = col < kH ? v : make_uint4(0, 0, 0, 0);
+                }
+#pragma unroll
+            for (int r = 0; r < kQkvRowsW; ++r) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KI; ++j) {
+                    const int col = j * 1024 + lane * 16;
+                    uint32_t x[8];
+                    if (col < kH) lds_pairs<16>(hs, col, x);
+                    else {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) x[i] = 0u;
+                    }
+                    acc = dot_fp8x16_bf16(x, sq[r][j], acc);
+                }
+                acc = wave_sum(acc);
+                if (lane == w * kQkvRowsW + r) rv = rbf(acc * load_scale<SK>(S, row + r));
+            }
+        }
+        if (lane < kQkvWgRows) sraw[qv][lane] = rv;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kQkvWgRows; ++i) {
+            const float f = __shfl(rv, i, kWave);
+            ss = fmaf(f, f, ss);
+        }
+        if (lane == 0) publish64(hslots + qv, tagged(tag, __float_as_uint(ss)));
+        return ss;
+    };
+    float part = 0.0f, tpart = 0.0f;  // tpart: lane qv's partial sum when qv was taken over
+    uint32_t taken = 0;               // siblings taken over
     const uint64_t tp = wall_clock64();
     for (;;) {
         const uint64_t v = collect64(hslots + min(lane, kQkvPerHead - 1));
-        part = __uint_as_float((uint32_t)v);
-        if (__all(lane >= kQkvPerHead || (uint32_t)(v >> 32) == tag)) break;
-        if (wall_clock64() - tp > kSpinTicks) {  // expired: store nothing rather than stale values
+        const bool took = lane < kQkvPerHead && ((taken >> lane) & 1u);
+        part = took ? tpart : __uint_as_float((uint32_t)v);
+        const uint64_t ms = __ballot(lane < kQkvPerHead && !took && (uint32_t)(v >> 32) != tag);
+        if (ms == 0) break;
+        const uint64_t dt = wall_clock64() - tp;
+        if (dt > kSpinTicks) {  // expired: store nothing rather than stale values
             if (lane == 0) atomicOr(err, kErrSpinTimeout);
             return;
+        }
+        if (__builtin_expect(dt > stall.steal_ticks, 0)) {
+            const int qv = __builtin_ctzll(ms);
+            if (lane == 0) atomicAdd(err + kErrTakeOvers, 1u);
+            const float ss = take_over(qv);
+            if (lane == qv) tpart = ss;
+            taken |= 1u << qv;
+            continue;
         }
         __builtin_amdgcn_s_sleep(1);
     }
@@ -812,22 +922,37 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
         return;
     }
     const int slot = (kv_off / (kNs * kDs * 2) + m0) % kTs;
-    float n = raw[min(lane, kQkvWgRows - 1)] * inv;
-    if (head < 24) n = n * wv;
-    n = rbf(n);
-    // y = bf16(bf16(x*cos) + bf16(x_swap*sin_dev)); the table's sin has its low half negated
-    // (generate_references.py:200-210), so x_swap is a plain half swap: slot i ^ 16 holds row t ^ 128.
-    const float partner = __shfl_xor(n, 16, kWave);
-    if (lane >= kQkvWgRows) return;
-    if (head >= 24) {
-        p.v_cache[(size_t)slot * (kNs * kDs) + (head - 24) * kDs + te] = (uint16_t)f2bf(n);
-        return;
+    // lane s < 32: slot s (head-local row t) from its raw value, norm weight and RoPE factors
+    auto emit = [&](float rawv, float wvv, float cvv, float svv, int t) {
+        float n = rawv * inv;
+        if (head < 24) n = n * wvv;
+        n = rbf(n);
+        // y = bf16(bf16(x*cos) + bf16(x_swap*sin_dev)); the table's sin has its low half negated
+        // (generate_references.py:200-210), so x_swap is a plain half swap: slot i ^ 16 holds row t ^ 128.
+        const float partner = __shfl_xor(n, 16, kWave);
+        if (lane >= kQkvWgRows) return;
+        if (head >= 24) {
+            p.v_cache[(size_t)slot * (kNs * kDs) + (head - 24) * kDs + t] = (uint16_t)f2bf(n);
+            return;
+        }
+        const float a = rbf(n * cvv);
+        const float b = rbf(partner * svv);
+        uint16_t* dst = head < 16 ? p.q_out + (size_t)m0 * kQs + head * kDs
+                                  : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs;
+        dst[t] = (uint16_t)f2bf(a + b);
+    };
+    emit(raw[min(lane, kQkvWgRows - 1)], wv, cv, sv, te);
+    while (taken) {
+        const int qv = __builtin_ctz(taken);
+        taken &= taken - 1;
+        const int tv = qkv_local_row(qv, min(lane, kQkvWgRows - 1));
+        const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
+        const int trow = rope_off / (kDs * 2) + m0;
+        const float wvv = wn ? bf2f(wn[tv]) : 1.0f;
+        const float cvv = head < 24 ? bf2f(p.cos[(size_t)trow * kDs + tv]) : 0.0f;
+        const float svv = head < 24 ? bf2f(p.sin[(size_t)trow * kDs + tv]) : 0.0f;
+        emit(sraw[qv][min(lane, kQkvWgRows - 1)], wvv, cvv, svv, tv);
     }
-    const float a = rbf(n * cv);
-    const float b = rbf(partner * sv);
-    uint16_t* dst = head < 16 ? p.q_out + (size_t)m0 * kQs + head * kDs
-                              : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs;
-    dst[te] = (uint16_t)f2bf(a + b);
 }
 
 // ===================================================================== O
@@ -906,17 +1031,22 @@ __global__ __launch_bounds__(kBlock) void o_decode_kernel(OParams p, int m0, uin
 // at once. Outputs and partial sums of squares leave through the tagged post-norm hand-off; the
 // kPostLeaders leaders apply post-norm and residual. The tag is the launch's epoch: the control
 // wave of workgroup b adds one to epoch counter b % 15 (16 workgroups per counter; epoch_tag).
+// A workgroup's outputs depend only on the attention row and the weights, so a leader that has
+// waited stall.steal_ticks computes a missing workgroup's outputs itself (a workgroup that was only
+// late publishes the same bits again); only leader g writes the residual rows of its group, so a
+// late leader still reads them unchanged.
 constexpr int kOWaves = 8;
 constexpr int kOBlock = 64 * kOWaves;
 constexpr int kORowsW = 2;  // rows per wave
 static_assert(kPostGrid * kPostWgRows == kH && kOWaves * kORowsW == kPostWgRows, "O grid");
 static_assert(kPostGrid == kOEpochCounters * kOEpochPer, "equal workgroups per epoch counter");
 
-template <ScaleKind SK, int KX>
+template <ScaleKind SK, int KX, bool Hold = false>
 __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, PostSlots* slots, uint32_t* tickets,
-                                                          uint32_t* err) {
+                                                          uint32_t* err, Stall stall) {
     __shared__ uint16_t xs[KX];
     __shared__ uint32_t dl[kPostWgRows];
+    if constexpr (Hold) stall_hold(stall);
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kOWaves - 1;
     const bool leader = blockIdx.x < kPostLeaders;
@@ -977,7 +1107,36 @@ __global__ __launch_bounds__(kOBlock) void o_fused_kernel(OParams p, int m0, Pos
     tag = __shfl(tag, 0, kWave);
     post_publish(slots, tag, dl, lane);
     if (!leader) return;
-    post_leader(slots, tag, res, r8, w8, false, 1.0f, lane, err);
+    // workgroup b's 16 outputs by this wave: two rows at a time, each row as b's waves compute it
+    auto steal = [&](int b) {
+        uint32_t v = 0;
+#pragma unroll 1
+        for (int r0 = 0; r0 < kPostWgRows; r0 += kORowsW) {
+            const int row = b * kPostWgRows + r0;
+            uint4 sq[kORowsW][KI];
+#pragma unroll
+            for (int r = 0; r < kORowsW; ++r)
+#pragma unroll
+                for (int j = 0; j < KI; ++j) sq[r][j] = ld_stream(p.ow + (size_t)(row + r) * KX + j * 1024 + lane * 16);
+            float sa[kORowsW];
+#pragma unroll
+            for (int r = 0; r < kORowsW; ++r) sa[r] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KI; ++j) {
+                uint32_t x[8];
+                lds_pairs<16>(xs, j * 1024 + lane * 16, x);
+#pragma unroll
+                for (int r = 0; r < kORowsW; ++r) sa[r] = dot_fp8x16_bf16(x, sq[r][j], sa[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < kORowsW; ++r) {
+                const float d = wave_sum(sa[r]);
+                if (lane == r0 + r) v = f2bf(d * load_scale<SK>(p.os, row + r));
+            }
+        }
+        post_publish_vals(slots, tag, b, v, lane);
+    };
+    post_leader(slots, tag, res, r8, w8, false, 1.0f, lane, err, stall.steal_ticks, steal);
 }
 
 // =================================================================== FFN
@@ -1027,13 +1186,18 @@ __device__ __forceinline__ float chunk_dot2(const uint32_t* x, const Chunk<F>& c
 }
 
 
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
 // Pre-RMSNorm of the residual row x into hs (whole block of NW waves), then the wave's kUgRL
 // up/gate row pairs -- L-rows lbase + g*lstride, g < kUgRL -- through a D-deep ring of loads:
 // D - 1 row pairs stay in flight while one is reduced. Returns, in lane g < kUgRL, GeGLU of
-// L-row lbase + g*lstride (before its bf16 rounding).
-template <FfnFormat F, ScaleKind SK, int NW>
+// L-row lbase + g*lstride (before its bf16 rounding). after_norm() runs once hs is complete.
+template <FfnFormat F, ScaleKind SK, int NW, typename H = NoHook>
 __device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t* __restrict__ x, int lbase,
-                                              int lstride, uint16_t* __restrict__ hs, float* __restrict__ red) {
+                                              int lstride, uint16_t* __restrict__ hs, float* __restrict__ red,
+                                              H after_norm = H{}) {
     constexpr int EPC = elems_per_chunk<F>();
     constexpr int RB = row_bytes<F>(kH);
     constexpr int SB = scale_row_bytes<F>(kH);
@@ -1068,6 +1232,7 @@ __device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t
     for (int g = 0; g < kUgPre; ++g) issue(g, ring[g]);
 
     rms_finish_bf16<NW>(st, hs, red);
+    after_norm();
 #pragma unroll
     for (int g = kUgPre; g < D - 1; ++g) issue(g, ring[g]);
     uint32_t xv[KI][EPC / 2];
@@ -1098,6 +1263,49 @@ __device__ __forceinline__ float up_gate_rows(const FfnParams& p, const uint16_t
         const float gate = proj_commit<F>(dg, __shfl(sg, g, kWave));
         // gemma4.py:197: bf16(bf16(gelu_tanh(gate)) * up)
         if (lane == g) pv = rbf(gelu_tanh(gate)) * up;
+    }
+    return pv;
+}
+
+// The same values as up_gate_rows for a row already normalised in hs, with one row pair in flight
+// and the activations read from LDS chunk by chunk: the take-over of another workgroup's rows,
+// where the caller's down prefetch and p words hold most registers. Same loads, same dot order.
+template <FfnFormat F, ScaleKind SK>
+__device__ __forceinline__ float up_gate_rows_lean(const FfnParams& p, int lbase, int lstride, const uint16_t* hs) {
+    constexpr int EPC = elems_per_chunk<F>();
+    constexpr int RB = row_bytes<F>(kH);
+    constexpr int SB = scale_row_bytes<F>(kH);
+    constexpr int KI = (RB + 1023) / 1024;
+    const int lane = lane_id();
+    float pv = 0.0f;
+#pragma unroll 1
+    for (int g = 0; g < kUgRL; ++g) {
+        const int l = lbase + g * lstride;
+        Chunk<F> c[2][KI];
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const bool valid = j * 1024 + lane * 16 < RB;
+            load_chunk<F>(c[0][j], p.up + (size_t)l * RB, (const uint8_t*)p.up_s + (size_t)l * SB, j, lane, valid);
+            load_chunk<F>(c[1][j], p.gate + (size_t)l * RB, (const uint8_t*)p.gate_s + (size_t)l * SB, j, lane, valid);
+        }
+        float du = 0.0f, dg = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            uint32_t x[EPC / 2];
+            const int e0 = j * 64 * EPC + lane * EPC;
+            if (e0 < kH) lds_pairs<EPC>(hs, e0, x);
+            else {
+#pragma unroll
+                for (int t = 0; t < EPC / 2; ++t) x[t] = 0u;
+            }
+            du = chunk_dot2<F>(x, c[0][j], du);
+            dg = chunk_dot2<F>(x, c[1][j], dg);
+        }
+        du = wave_sum(du);
+        dg = wave_sum(dg);
+        const float up = proj_commit<F>(du, row_scale<F, SK>(p.up_s, p.up_g, l));
+        const float gate = proj_commit<F>(dg, row_scale<F, SK>(p.gate_s, p.gate_g, l));
+        if (lane == g) pv = rbf(gelu_tanh(gate)) * up;  // gemma4.py:197
     }
     return pv;
 }
@@ -1147,6 +1355,18 @@ __device__ __forceinline__ void down_chunk_issue(Chunk<F> (&dst)[R], const FfnPa
 //
 // Every poll is bounded by the wall clock (kSpinTicks): on expiry it sets kErrSpinTimeout in the
 // device error word and carries on, so every wave exits even if the grid were not resident.
+//
+// Waits that last stall.steal_ticks take the missing work over, so the launch completes correctly
+// with any part of its grid resident:
+//   * p: a waiting workgroup computes a missing block's 64 GeGLU values from its own normalised
+//     row and publishes them. Each block's values are published by exactly one workgroup, the
+//     first to exchange the launch's tag into the block's claim word (the owner does so as soon as
+//     its norm is done, long before any wait could expire). An owner that loses the exchange
+//     started late and may have read residual rows the leaders had already rewritten; it
+//     publishes nothing.
+//   * post-norm: a leader computes a missing workgroup's down outputs from p and publishes them
+//     (the same bits as the owner's, which depend only on p and the weights).
+//   * Leader g alone writes the residual rows of its group, so a late leader finds them unchanged.
 constexpr int kFfnWaves = 8;
 constexpr int kFfnBlock = 64 * kFfnWaves;
 constexpr int kFfnGrid = kL / (kFfnWaves * kUgRL);  // 240 workgroups
@@ -1165,16 +1385,24 @@ __device__ __forceinline__ void reload_stale(uint64_t (&w)[N], uint32_t tag, A a
     ((w[I] = (uint32_t)(w[I] >> 32) != tag ? collect64(addr(I)) : w[I]), ...);
 }
 
-template <FfnFormat F, ScaleKind SK>
+// word w of thread t in read i of the p words: workgroups start at different words (rotation by
+// 32 b), so that 240 readers of the same 61 KB do not request the same lines at the same time
+__device__ __forceinline__ int ffn_pword(int i) { return (threadIdx.x + kFfnBlock * i + blockIdx.x * 32) % (kL / 2); }
+
+template <FfnFormat F, ScaleKind SK, bool Hold = false>
 __global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uint32_t* tickets, uint32_t* err) {
+void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uint32_t* tickets, uint32_t* err,
+                      Stall stall) {
     constexpr int KD = down_chunks<F>();
     constexpr int EPC = elems_per_chunk<F>();
     __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
+    __shared__ uint16_t sx[kH];  // normalised x, kept for a take-over of another block's rows
     __shared__ float red[kFfnWaves];
     __shared__ float pl[kFfnWaves * kUgRL];
     __shared__ uint32_t dl[kFfnWgRows];  // the workgroup's down outputs (bf16 bits)
-    __shared__ uint32_t s_tag, s_expired;
+    __shared__ uint32_t s_tag, s_expired, s_stall;
+    __shared__ int s_victim;
+    if constexpr (Hold) stall_hold(stall);
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
     const bool leader = blockIdx.x < kPostLeaders;
@@ -1205,13 +1433,24 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         }
     }
 
-    // ---- up/gate: stage g reads L-rows base + 8g + wave; lane g's value is GeGLU row 8g + wave
+    // ---- up/gate: stage g reads L-rows base + 8g + wave; lane g's value is GeGLU row 8g + wave.
+    // Once the norm is done the block's claim goes out (its return arrives behind the first stage)
+    // and the normalised row is copied aside.
+    uint32_t claim_old = 0;
+    auto claim = [&] {
+        if (ctl && lane == 0)
+            claim_old = __hip_atomic_exchange(reinterpret_cast<uint32_t*>(&slots->claim[blockIdx.x]), ep_tag,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x < kH / 8)
+            reinterpret_cast<uint4*>(sx)[threadIdx.x] = reinterpret_cast<const uint4*>(sh)[threadIdx.x];
+    };
     const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
-    const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red);
+    const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red, claim);
     if (lane < kUgRL) pl[lane * kFfnWaves + wave] = pv;
     if (ctl && lane == 0) {
         s_tag = ep_tag;
         s_expired = 0u;
+        s_stall = 0u;
     }
     __syncthreads();  // pl complete; every wave has read its x out of sh
     const uint32_t tag = s_tag;
@@ -1228,15 +1467,16 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         // its loads in order, so they are not queued behind this workgroup's weight loads. Every
         // wave (the control wave too) then issues its first PD down chunks and every thread its
         // first read of p; words not yet current are read again until they are.
-        if (ctl && lane < kFfnWaves * kUgRL / 2)
-            publish64(ptag + blockIdx.x * (kFfnWaves * kUgRL / 2) + lane,
-                      tagged(tag, pk_bf16(pl[2 * lane], pl[2 * lane + 1])));
+        if (ctl) {
+            const bool won = __shfl(claim_old, 0, kWave) != tag;
+            if (won && lane < kFfnWaves * kUgRL / 2)
+                publish64(ptag + blockIdx.x * (kFfnWaves * kUgRL / 2) + lane,
+                          tagged(tag, pk_bf16(pl[2 * lane], pl[2 * lane + 1])));
+        }
         __syncthreads();  // the publish is issued ahead of every load below
         constexpr int PW = kL / 2 / kFfnBlock;  // 15 words per thread
         static_assert(PW * kFfnBlock == kL / 2, "p words per thread");
-        // word w of thread t in read i: workgroups start at different words (rotation by 32 b), so
-        // that 240 readers of the same 61 KB do not request the same lines at the same time
-        auto pword = [&](int i) { return (threadIdx.x + kFfnBlock * i + blockIdx.x * 32) % (kL / 2); };
+        auto pword = [](int i) { return ffn_pword(i); };
         // The down prefetch goes out first and the reads of p behind it: a CU returns its loads in
         // order, so a read of p issued ahead of the prefetch would come back early, find the words
         // of the slowest workgroups not yet published, and its re-read would then queue behind the
@@ -1247,26 +1487,99 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
 #pragma unroll
         for (int i = 0; i < PW; ++i) pw[i] = collect64(ptag + pword(i));
         const uint64_t t0 = wall_clock64();
+        bool stalled = false;
         for (;;) {
             bool ok = true;
 #pragma unroll
             for (int i = 0; i < PW; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
             if (__all(ok)) break;
-            if (wall_clock64() - t0 > kSpinTicks) {
+            const uint64_t dt = wall_clock64() - t0;
+            if (dt > kSpinTicks) {
                 if (lane == 0) {
                     atomicOr(err, kErrSpinTimeout);
                     s_expired = 1u;
                 }
                 break;
             }
+            if (__builtin_expect(dt > stall.steal_ticks, 0)) {
+                stalled = true;
+                if (lane == 0) s_stall = 1u;
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
             // reload the words still carrying an older tag (unrolled at compile time)
             reload_stale(pw, tag, [&](int i) { return ptag + pword(i); }, std::make_integer_sequence<int, PW>{});
         }
+        if (!stalled) {
 #pragma unroll
-        for (int i = 0; i < PW; ++i) *reinterpret_cast<uint32_t*>(sh + 2 * pword(i)) = (uint32_t)pw[i];
+            for (int i = 0; i < PW; ++i) *reinterpret_cast<uint32_t*>(sh + 2 * pword(i)) = (uint32_t)pw[i];
+        }
+        __syncthreads();  // p staged, unless a wave stalled
+        if (__builtin_expect(s_stall && !s_expired, 0)) {
+            // Every wave of the workgroup together: the control wave finds the blocks whose first
+            // word is stale (a block whose first word is current has an owner that is publishing
+            // it), claims one, and the workgroup computes its values from the copy of the
+            // normalised row and publishes them; until every word carries the tag.
+            for (;;) {
+                reload_stale(pw, tag, [&](int i) { return ptag + pword(i); }, std::make_integer_sequence<int, PW>{});
+                bool ok = true;
+#pragma unroll
+                for (int i = 0; i < PW; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
+                if (__syncthreads_and(ok)) break;
+                if (ctl) {
+                    constexpr int NB = (kFfnGrid + kWave - 1) / kWave;
+                    uint64_t cand[NB];
+#pragma unroll
+                    for (int i = 0; i < NB; ++i) {
+                        const int b = lane + kWave * i;
+                        const uint64_t w0 = collect64(ptag + min(b, kFfnGrid - 1) * 32);
+                        cand[i] = __ballot(b < kFfnGrid && (uint32_t)(w0 >> 32) != tag);
+                    }
+                    int victim = -1;
+                    if (wall_clock64() - t0 > kSpinTicks) {
+                        if (lane == 0) atomicOr(err, kErrSpinTimeout);
+                        victim = -2;
+                    } else if (lane == 0) {
+                        for (int i = 0; i < NB && victim < 0; ++i)
+                            for (uint64_t m = cand[i]; m && victim < 0; m &= m - 1) {
+                                const int b = kWave * i + __builtin_ctzll(m);
+                                if (__hip_atomic_exchange(reinterpret_cast<uint32_t*>(&slots->claim[b]), tag,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag)
+                                    victim = b;
+                            }
+                    }
+                    if (lane == 0) {
+                        if (victim == -2) s_expired = 1u;
+                        if (victim >= 0) atomicAdd(err + kErrTakeOvers, 1u);
+                        s_victim = victim;
+                    }
+                }
+                __syncthreads();
+                const int victim = s_victim;
+                if (victim == -2) break;
+                if (victim < 0) {
+                    __builtin_amdgcn_s_sleep(8);
+                    continue;
+                }
+                const float vv = up_gate_rows_lean<F, SK>(p, victim * (kFfnWaves * kUgRL) + wave, kFfnWaves, sx);
+                if (lane < kUgRL) pl[lane * kFfnWaves + wave] = vv;
+                __syncthreads();
+                // the next round reads the words back (the block's claim keeps it from being taken
+                // again while they become visible)
+                if (ctl && lane < kFfnWaves * kUgRL / 2)
+                    publish64(ptag + victim * (kFfnWaves * kUgRL / 2) + lane,
+                              tagged(tag, pk_bf16(pl[2 * lane], pl[2 * lane + 1])));
+                __syncthreads();  // pl is free again
+            }
+#pragma unroll
+            for (int i = 0; i < PW; ++i) *reinterpret_cast<uint32_t*>(sh + 2 * pword(i)) = (uint32_t)pw[i];
+            // The down prefetch again: the take-over used its registers (and with them, its
+            // values are not kept live through the take-over).
+#pragma unroll
+            for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
+            __syncthreads();  // p staged
+        }
     }
-    __syncthreads();  // p staged
 
     // ---- down: the ring streams the rest of the rows while the dots run
     {
@@ -1312,7 +1625,43 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
     }
     post_publish(slots, tag, dl, lane);
     if (!leader) return;
-    post_leader(slots, tag, res, r8, w8, p.layer_scalar != nullptr, lsv, lane, err);
+    // workgroup b's 16 down outputs by this wave: two rows at a time, each row as b's waves compute
+    // it (the chunks in order, kSB loads of each row in flight)
+    auto steal = [&](int b) {
+        constexpr int kSB = 4;
+        uint32_t v = 0;
+#pragma unroll 1
+        for (int r0 = 0; r0 < kFfnWgRows; r0 += kFfnDownR) {
+            const int drow = b * kFfnWgRows + r0;
+            float acc[kFfnDownR];
+#pragma unroll
+            for (int r = 0; r < kFfnDownR; ++r) acc[r] = 0.0f;
+#pragma unroll 1
+            for (int j0 = 0; j0 < KD; j0 += kSB) {
+                Chunk<F> c[kSB][kFfnDownR];
+#pragma unroll
+                for (int jj = 0; jj < kSB; ++jj)
+                    if (j0 + jj < KD) down_chunk_issue<F, kFfnDownR>(c[jj], p, drow, kFfnDownR, j0 + jj, lane);
+#pragma unroll
+                for (int jj = 0; jj < kSB; ++jj) {
+                    const int e0 = (j0 + jj) * 64 * EPC + lane * EPC;
+                    if (j0 + jj < KD && e0 < kL) {
+                        uint32_t x[EPC / 2];
+                        lds_pairs<EPC>(sh, e0, x);
+#pragma unroll
+                        for (int r = 0; r < kFfnDownR; ++r) acc[r] = chunk_dot2<F>(x, c[jj][r], acc[r]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < kFfnDownR; ++r) {
+                const float dsum = wave_sum(acc[r]);
+                if (lane == r0 + r) v = f2bf(proj_commit<F>(dsum, row_scale<F, SK>(p.down_s, p.down_g, drow + r)));
+            }
+        }
+        post_publish_vals(slots, tag, b, v, lane);
+    };
+    post_leader(slots, tag, res, r8, w8, p.layer_scalar != nullptr, lsv, lane, err, stall.steal_ticks, steal);
 }
 
 // ========================================================== raw projection
@@ -1389,22 +1738,34 @@ hipError_t launch(K kernel, dim3 grid, hipStream_t s, A... args) {
 template <typename K>
 static bool fits_resident(int8_t& known, K kernel, int block, int grid, const DevCtx* ctx);
 
+// The waits' take-over threshold (and, in tests, held workgroups) passed to every single-launch
+// kernel.
+static Stall g_stall = {kStealTicks, 0, {-1, -1, -1, -1}};
+
+void set_stall(const Stall& st) { g_stall = st; }
+
+// A single-launch kernel, or its Hold instantiation while a test holds workgroups.
+template <typename K, typename KH, typename... A>
+static hipError_t launch_fused(K kernel, KH kernel_hold, dim3 grid, int block, hipStream_t s, A... args) {
+    if (g_stall.hold_ticks) hipLaunchKernelGGL(kernel_hold, grid, dim3(block), 0, s, args..., g_stall);
+    else hipLaunchKernelGGL(kernel, grid, dim3(block), 0, s, args..., g_stall);
+    return hipGetLastError();
+}
+
 hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* ctx) {
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
         if (mm == 1) {
             const bool f32 = p.scale_kind == ScaleKind::F32;
             if (f32 && fits_resident(ctx->qkv_fused[0], qkv_fused_kernel<ScaleKind::F32>, kQkvBlock, kQkvGrid, ctx)) {
-                qkv_fused_kernel<ScaleKind::F32><<<dim3(kQkvGrid), dim3(kQkvBlock), 0, s>>>(p, m0, ctx->qkv_part,
-                                                                                           ctx->tickets, ctx->err);
-                const hipError_t e = hipGetLastError();
+                const hipError_t e = launch_fused(qkv_fused_kernel<ScaleKind::F32>, qkv_fused_kernel<ScaleKind::F32, true>,
+                                                  dim3(kQkvGrid), kQkvBlock, s, p, m0, ctx->qkv_part, ctx->tickets, ctx->err);
                 if (e != hipSuccess) return e;
                 continue;
             }
             if (!f32 && fits_resident(ctx->qkv_fused[1], qkv_fused_kernel<ScaleKind::BF16>, kQkvBlock, kQkvGrid, ctx)) {
-                qkv_fused_kernel<ScaleKind::BF16><<<dim3(kQkvGrid), dim3(kQkvBlock), 0, s>>>(p, m0, ctx->qkv_part,
-                                                                                            ctx->tickets, ctx->err);
-                const hipError_t e = hipGetLastError();
+                const hipError_t e = launch_fused(qkv_fused_kernel<ScaleKind::BF16>, qkv_fused_kernel<ScaleKind::BF16, true>,
+                                                  dim3(kQkvGrid), kQkvBlock, s, p, m0, ctx->qkv_part, ctx->tickets, ctx->err);
                 if (e != hipSuccess) return e;
                 continue;
             }
@@ -1461,16 +1822,14 @@ static hipError_t o_decode_impl(const OParams& p, int M, hipStream_t s, DevCtx* 
             const bool f32 = p.scale_kind == ScaleKind::F32;
             PostSlots* slots = reinterpret_cast<PostSlots*>(ctx->o_part);
             if (f32 && fits_resident(fused_known[0], o_fused_kernel<ScaleKind::F32, KX>, kOBlock, kPostGrid, ctx)) {
-                o_fused_kernel<ScaleKind::F32, KX><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets,
-                                                                                            ctx->err);
-                const hipError_t e = hipGetLastError();
+                const hipError_t e = launch_fused(o_fused_kernel<ScaleKind::F32, KX>, o_fused_kernel<ScaleKind::F32, KX, true>,
+                                                  dim3(kPostGrid), kOBlock, s, p, m0, slots, ctx->tickets, ctx->err);
                 if (e != hipSuccess) return e;
                 continue;
             }
             if (!f32 && fits_resident(fused_known[1], o_fused_kernel<ScaleKind::BF16, KX>, kOBlock, kPostGrid, ctx)) {
-                o_fused_kernel<ScaleKind::BF16, KX><<<dim3(kPostGrid), dim3(kOBlock), 0, s>>>(p, m0, slots, ctx->tickets,
-                                                                                             ctx->err);
-                const hipError_t e = hipGetLastError();
+                const hipError_t e = launch_fused(o_fused_kernel<ScaleKind::BF16, KX>, o_fused_kernel<ScaleKind::BF16, KX, true>,
+                                                  dim3(kPostGrid), kOBlock, s, p, m0, slots, ctx->tickets, ctx->err);
                 if (e != hipSuccess) return e;
                 continue;
             }
@@ -1516,9 +1875,8 @@ static hipError_t ffn_decode_impl(const FfnParams& p, int M, hipStream_t s, DevC
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
         hipError_t e;
         if (mm == 1 && ffn_fused_fits<F, SK>(ctx)) {
-            ffn_fused_kernel<F, SK><<<dim3(kFfnGrid), dim3(kFfnBlock), 0, s>>>(
-                p, m0, ctx->ffn_ptag, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
-            e = hipGetLastError();
+            e = launch_fused(ffn_fused_kernel<F, SK>, ffn_fused_kernel<F, SK, true>, dim3(kFfnGrid), kFfnBlock, s, p, m0,
+                             ctx->ffn_ptag, reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
             if (e != hipSuccess) return e;
             continue;
         }

@@ -49,16 +49,17 @@ constexpr int kFaSplitPages = 8;                           // the fused pass spl
 constexpr int kFattnRecords = 256;                         // records of scratch (>= kMaxDecodeM * kFaChunks)
 constexpr size_t kFattnPartFloats = (size_t)kFattnRecords * kFaRec;
 
-// Tagged hand-off words of the single-launch FFN (per workgroup a partial sum and 8 output words;
-// never shared with another kernel).
+// Tagged hand-off words of the single-launch FFN (per workgroup a partial sum, 8 output words and
+// a claim word; never shared with another kernel).
 constexpr int kFfnPartSlots = 256;
-constexpr int kFfnSlotWords = kFfnPartSlots * 9;
+constexpr int kFfnSlotWords = kFfnPartSlots * 10;
 constexpr int kQkvSlotWords = 32 * 8;
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
 constexpr uint32_t kErrKvOffset = 2u;
 constexpr uint32_t kErrSpinTimeout = 4u;
+constexpr int kErrTakeOvers = 1;  // err[1]: waits of the one-token kernels that took work over (tests)
 
 // Per-device persistent scratch, allocated once on first use (never per call).
 struct DevCtx {
@@ -105,6 +106,19 @@ struct OParams {
     uint16_t* residual;
     const float* div = nullptr;  // full-attention layers: running softmax sums [M][16] that divide x
 };
+
+// Waits of the single-launch kernels (a kernel argument). A workgroup that has waited steal_ticks
+// (100 MHz wall clock) for another workgroup of its grid does that workgroup's work itself, so the
+// kernels finish with correct results even when part of the grid cannot be resident (another
+// process holding CUs). Test only: workgroups hold[0..3] of each launch wait hold_ticks at entry,
+// before they read or write anything, as if they had started late.
+struct Stall {
+    uint32_t steal_ticks;
+    uint32_t hold_ticks;
+    int32_t hold[4];
+};
+constexpr uint32_t kStealTicks = 50000;  // 500 us: far beyond any wait of a resident grid
+void set_stall(const Stall& st);           // the Stall every later single-launch call passes (tests)
 
 struct FfnParams {
     FfnFormat fmt;
