@@ -709,12 +709,16 @@ __global__ __launch_bounds__(kBlock) void qkv_decode_kernel(QkvParams p, int m0,
 // ------------------------------------------------------------ QKV: single launch (one token row)
 // 256 workgroups of nine waves: eight compute four rows each and the ninth (the control wave)
 // normalises the activation row and finishes the head. Workgroup b computes 32 rows of head
-// h = b / 8 -- rows 16q .. 16q+15 and 128+16q .. 128+16q+15 of the head for q = b % 8, so every
-// row's RoPE partner (t ^ 128) is in the same workgroup. The head's RMSNorm needs the sum of
-// squares of all 256 rows: each workgroup publishes its partial sum tagged with the launch's
-// epoch (the head's epoch counter gets one add per workgroup at entry; epoch_tag) and polls the
-// head's 8 tagged words. Then the
-// control wave normalises, rotates and stores the workgroup's 32 values.
+// h = b % 32 -- rows 16q .. 16q+15 and 128+16q .. 128+16q+15 of the head for q = b / 32, so every
+// row's RoPE partner (t ^ 128) is in the same workgroup. The dispatcher deals workgroups to the
+// 8 XCDs round-robin (XCD = b % 8), so a head's 8 workgroups share one XCD and its exchange
+// never crosses to the other I/O die: an agent-scope round trip between two workgroups measured
+// about 635 ns on one XCD and 1015 ns across the dies, and the kernel 9.0 against 9.3 us with
+// h = b / 8. Only latency depends on this placement, not the result.
+// The head's RMSNorm needs the sum of squares of all 256 rows: each workgroup publishes its
+// partial sum tagged with the launch's epoch (the head's epoch counter gets one add per workgroup
+// at entry; epoch_tag) and polls the head's 8 tagged words. Then the control wave normalises,
+// rotates and stores the workgroup's 32 values.
 // Every output depends only on the inputs (nothing is read that the launch writes), so a control
 // wave that has waited stall.steal_ticks for a sibling's partial sum computes that sibling's 32 rows
 // itself, publishes their partial sum and stores their outputs too; a sibling that was only late
@@ -741,7 +745,7 @@ __global__ __launch_bounds__(kQkvBlock) void qkv_fused_kernel(QkvParams p, int m
     if constexpr (Hold) stall_hold(stall);
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kQkvWaves;
-    const int head = blockIdx.x / kQkvPerHead, q = blockIdx.x % kQkvPerHead;
+    const int head = blockIdx.x % 32, q = blockIdx.x / 32;
 
     // the wave's four consecutive rows (the control wave's are never loaded)
     const int t0 = qkv_local_row(q, min(wave, kQkvWaves - 1) * kQkvRowsW);

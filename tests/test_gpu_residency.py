@@ -70,11 +70,11 @@ def calls():
 
 
 # (label, steal ticks, held workgroups, take-overs expected). 2, 100, 239: an O/FFN leader, a
-# middle and the last workgroup of the 240-workgroup grids (QKV: heads 0, 12 and 29); 255: QKV's
-# last. 0, 1: two leaders; 130, 131: two workgroups of one QKV head.
+# middle and the last workgroup of the 240-workgroup grids (QKV, head b % 32: heads 2, 4 and 15);
+# 255: QKV's last. 0, 1: two leaders; 130, 162: two workgroups of QKV head 2.
 CASES = [
     ("take-over", STEAL, (2, 100, 239, 255), True),
-    ("leaders late", STEAL, (0, 1, 130, 131), True),
+    ("leaders late", STEAL, (0, 1, 130, 162), True),
     ("slow, no take-over", 10 * HOLD, (2, 100, 239, 255), False),
 ]
 
