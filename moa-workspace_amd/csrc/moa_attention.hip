@@ -12,11 +12,14 @@
 // unless masked slots hold scores far above the valid ones. Here the max is taken over the valid
 // slots only. A row with no valid slot returns zeros.
 //
-// Split over slots ("flash decoding"): workgroup (c, n, m) takes the 32 slots 32 c .. 32 c + 31
+// Split over slots ("flash decoding"): workgroup (n, c, m) takes the 32 slots 32 c .. 32 c + 31
 // of head n for token row m. It computes its partial (max, sum of exp, sum of exp * v) for both
 // query heads and publishes it with agent-scope stores. Then it adds one to the head's ticket
 // counter; the workgroup that completes the head's 32 (the counter's old value is 31 mod 32)
 // combines the partials. Nothing waits on another workgroup, so residency is not required.
+// The head is the grid's x index: workgroups go to the 8 XCDs round-robin by linear index, so all
+// 32 of head n run on XCD n and its ticket and partials never cross XCDs (7.10 -> 6.96 us per
+// call against the chunk as x index; the results do not depend on the placement).
 #include <hip/hip_runtime.h>
 
 #include "moa_device.h"
@@ -48,7 +51,7 @@ __global__ __launch_bounds__(kAtBlock) void attn_split_kernel(const uint16_t* __
     __shared__ float ored[8][kGs][kDs];       // per slot group partial o
     __shared__ uint32_t s_last;
     const int t = threadIdx.x;
-    const int c = blockIdx.x, n = blockIdx.y, m = blockIdx.z;
+    const int n = blockIdx.x, c = blockIdx.y, m = blockIdx.z;
     const int t0 = c * kAtSlots;
     const uint16_t* qrow = q + ((size_t)m * kNs + n) * kGs * kDs;
     // The chunk's K and V rows and its mask values are requested first (none depends on q); q
@@ -224,7 +227,7 @@ hipError_t launch_sliding_attention(const uint16_t* q, const uint16_t* k_cache, 
                                     uint16_t* out, int M, hipStream_t s, DevCtx* ctx) {
     for (int m0 = 0; m0 < M; m0 += kMaxDecodeM) {
         const int mm = M - m0 < kMaxDecodeM ? M - m0 : kMaxDecodeM;
-        hipLaunchKernelGGL(attn_split_kernel, dim3(kAtChunks, kNs, mm), dim3(kAtBlock), 0, s,
+        hipLaunchKernelGGL(attn_split_kernel, dim3(kNs, kAtChunks, mm), dim3(kAtBlock), 0, s,
                            q + (size_t)m0 * kQs, k_cache, v_cache, mask + (size_t)m0 * kTs, out + (size_t)m0 * kQs,
                            ctx->attn_part, ctx->tickets + kTicketAttn * kTicketStride);
         const hipError_t e = hipGetLastError();
