@@ -107,5 +107,11 @@ def check(code: int) -> None:
         raise MoaError(code, load().moa_last_error_string().decode())
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
-    check(getattr(load(), name)(*args))
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    check(fn(*args))

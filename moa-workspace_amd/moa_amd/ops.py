@@ -23,11 +23,14 @@ H, L, NS, GS, DS, QS, PS, TS, E, W = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 3
 
 
 def _ptr(t: torch.Tensor | None, name: str, dtypes, numel: int | None = None):
+    """The tensor's device address after the checks (an int: the signatures declare void*, so
+    ctypes converts it). The cheapest torch attributes are used: every operator call runs this for
+    each of its tensors, and `t.device` alone costs about 0.4 us per tensor."""
     if t is None:
         return None
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"{name} must live on a ROCm device, got {t.device}")
     if t.dtype not in dtypes:
         raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
@@ -35,7 +38,7 @@ def _ptr(t: torch.Tensor | None, name: str, dtypes, numel: int | None = None):
         raise ValueError(f"{name} must be contiguous")
     if numel is not None and t.numel() != numel:
         raise ValueError(f"{name}: expected {numel} elements, got {t.numel()}")
-    return C.c_void_p(t.data_ptr())
+    return t.data_ptr()
 
 
 _BF16 = (torch.bfloat16, torch.int16, torch.uint16)
@@ -44,8 +47,9 @@ _F32 = (torch.float32,)
 _I32 = (torch.int32,)
 
 
-def _stream(t: torch.Tensor) -> C.c_void_p:
-    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+def _stream(t: torch.Tensor) -> int:
+    """The current HIP stream of the tensor's device (its handle as an int)."""
+    return torch.cuda.current_stream(t.get_device()).cuda_stream
 
 
 def _rows(x: torch.Tensor, width: int, name: str) -> int:
