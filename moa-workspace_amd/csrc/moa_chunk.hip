@@ -475,6 +475,16 @@ __global__ __launch_bounds__(kCkBlock) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
 }
 
+// Rows of the A-tile producers. A 128-byte line of a tile holds one 16-byte unit of each of 8
+// consecutive rows, so with one workgroup per row each line is written by 8 workgroups; they are
+// dealt to the 8 XCDs round-robin (XCD = b % 8), and rows 8g .. 8g + 7 go to workgroups on XCD
+// g % 8, where one L2 assembles the whole line. Rows past the last multiple of 64 keep b.
+__device__ __forceinline__ int tile_row(int b, int M) {
+    if (b >= (M & ~63)) return b;
+    const int x = b & 7, j = b >> 3;
+    return ((x + 8 * (j >> 3)) << 3) | (j & 7);
+}
+
 // Block sum over the four waves, in wave order.
 __device__ __forceinline__ float ck_block_sum(float v, float* red) {
     v = wave_sum(v);
@@ -485,13 +495,14 @@ __device__ __forceinline__ float ck_block_sum(float v, float* red) {
 }
 
 // out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) (gemma4.py:83-89), written as A tiles
-// (Tiles) or row-major [M][kH]. One workgroup per row; thread t < 240 owns elements 16t .. 16t+15.
+// (Tiles) or row-major [M][kH]. One workgroup per row (for tiles, row tile_row(b)); thread t < 240
+// owns elements 16t .. 16t+15.
 template <bool Tiles = true>
 __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint16_t* __restrict__ x,
                                                                       const uint16_t* __restrict__ w,
                                                                       uint16_t* __restrict__ out) {
     __shared__ float red[4];
-    const int t = threadIdx.x, m = blockIdx.x;
+    const int t = threadIdx.x, m = Tiles ? tile_row(blockIdx.x, gridDim.x) : blockIdx.x;
     const bool act = t < kH / 16;
     const int c = min(t, kH / 16 - 1);
     const uint16_t* xr = x + (size_t)m * kH + c * 16;
@@ -518,10 +529,10 @@ __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint
 }
 
 // Row-major bf16 [M][K] -> A tiles (the O-projection's input arrives row-major). One workgroup
-// per row; thread t moves 16-byte units t, t + 256, ...
+// per row (tile_row); thread t moves 16-byte units t, t + 256, ...
 __global__ __launch_bounds__(kCkBlock) void chunk_tile_rows_kernel(const uint16_t* __restrict__ x, int K,
                                                                    uint16_t* __restrict__ out) {
-    const int m = blockIdx.x;
+    const int m = tile_row(blockIdx.x, gridDim.x);
     for (int u = threadIdx.x; u < K / 8; u += kCkBlock)
         *reinterpret_cast<uint4*>(out + atile_off(m, u * 8, K)) = ld16(x + (size_t)m * K + u * 8);
 }
