@@ -687,8 +687,9 @@ int pick_splits(int tiles, int ksteps, size_t rows_x_cols) {
 // Weight rows per workgroup of a split-K projection. The O projection (K = 4096) takes 64: twice
 // the tiles of 128-row tiles, so half the k splits fill the device and half the f32 partial sums
 // are written and read back (measured at M = 256: GEMM 17.3 -> 16.5 us, post rows 9.1 -> 6.9 us).
-// QKV and down keep 128, whose main loop does twice the MFMA work per A load and per barrier
-// (with 64, down measured 39.1 -> 44.6 us against 9.5 -> 7.1 us saved in its post rows).
+// QKV takes 64 up to 256 rows (launch_qkv_chunk). Down keeps 128, whose main loop does twice the
+// MFMA work per A load and per barrier (with 64, down measured 39.1 -> 44.6 us against 9.5 ->
+// 7.1 us saved in its post rows).
 constexpr int kCkOBN = 64;
 
 template <FfnFormat F = FfnFormat::FP8, int BN = kCkBN>
@@ -730,8 +731,13 @@ hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, De
     g.w[0] = p.qw; g.w[1] = p.kw; g.w[2] = p.vw;
     g.nseg[0] = 0; g.nseg[1] = kQs; g.nseg[2] = kQs + kPs; g.nseg[3] = kQkvRowsTotal; g.nsegs = 3;
     g.yf = ctx->fbuf;
-    const int sp = pick_splits(kQkvRowsTotal / kCkBN * m_tiles(M), kH / kCkBK, (size_t)M * kQkvRowsTotal);
-    e = gemm_partial(g, sp, p.scale_kind, s);
+    // Up to 256 rows, 64-row weight tiles (128 tiles x 2 k splits instead of 64 x 4: half the
+    // partial sums; M = 256: 39.3 -> 37.4 us). Beyond, they would not split, and the 512 tiles
+    // of M = 1024 measured 112 us against 102 with 128-row tiles.
+    const bool narrow = m_tiles(M) == 1;
+    const int sp = pick_splits(kQkvRowsTotal / (narrow ? kCkOBN : kCkBN) * m_tiles(M), kH / kCkBK,
+                               (size_t)M * kQkvRowsTotal);
+    e = narrow ? gemm_partial<FfnFormat::FP8, kCkOBN>(g, sp, p.scale_kind, s) : gemm_partial(g, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
     if (sp <= 2) return launch_qkv_heads(p, m0, M, ctx->fbuf, sp, s, ctx);
     const float* part = ctx->fbuf;
