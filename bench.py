@@ -104,11 +104,16 @@ def main() -> int:
                              "chunk", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time torch.matmul (the vendor bf16 GEMM) on the chunk's four GEMM shapes with "
+                         "bf16 weights, as a reference point for the MFMA path; prints one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the hot path is a per-GPU kernel; "
                                    "run with --gpus 1 (multi-GPU sharding is a design note only)"}))
         return 2
+    if args.vendor_gemm:
+        return vendor_gemm(args.chunk_rows or 256)
 
     import numpy as np
     import torch
@@ -552,6 +557,43 @@ FLOOR_SEQUENCE = [  # (label, bytes, workgroups, threads) in dispatch order for 
     ("empty o/ffn shape", 0, 240, 512), ("empty qkv shape", 0, 256, 576),
     ("read o weights", WEIGHT_BYTES["o"], 240, 512), ("read qkv weights", WEIGHT_BYTES["qkv"], 256, 576),
     ("read ffn weights", WEIGHT_BYTES["ffn"], 240, 512), ("read 1 GiB", 1 << 30, 1024, 512)]
+
+
+def vendor_gemm(rows: int) -> int:
+    """The vendor bf16 GEMM (torch.matmul, which calls hipBLASLt) on the config-4 chunk's GEMM shapes:
+    X [rows, K] bf16 times W [N, K]^T with bf16 weights (twice the bytes of FP8), copies rotated over
+    >= 512 MiB, 20 calls per HIP graph, median of 10 replays. Nothing of the library runs here: it
+    is a reference point for what a library GEMM reaches on these shapes."""
+    import numpy as np
+    import torch
+
+    torch.cuda.set_device(0)
+    out = {}
+    for name, n, k in (("up+gate", 2 * 15360, 3840), ("down", 3840, 15360), ("qkv", 8192, 3840), ("o", 3840, 4096)):
+        x = torch.randn(rows, k, device="cuda", dtype=torch.bfloat16)
+        ws = [torch.randn(n, k, device="cuda", dtype=torch.bfloat16) for _ in range(max(2, -(-(512 << 20) // (n * k * 2))))]
+        for i in range(3):
+            x @ ws[i % len(ws)].t()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(20):
+                x @ ws[i % len(ws)].t()
+        g.replay()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(11)]
+        ev[0].record()
+        for r in range(10):
+            g.replay()
+            ev[r + 1].record()
+        torch.cuda.synchronize()
+        us = float(np.median([ev[r].elapsed_time(ev[r + 1]) / 20 * 1e3 for r in range(10)]))
+        tf = 2 * rows * n * k / us / 1e6
+        out[name] = {"N": n, "K": k, "us": round(us, 2), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        log(f"vendor bf16 GEMM {name:8} M={rows} N={n} K={k}: {us:8.2f} us  {tf:7.1f} TFLOP/s")
+        del ws, g
+    print(json.dumps({"vendor_gemm": {"rows": rows, "weights": "bf16", "ops": out}}))
+    return 0
 
 
 def floor_profile(torch, steps: int) -> None:
