@@ -592,6 +592,72 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads_kernel(QkvParams p, 
     dst[t] = (uint16_t)f2bf(a + b);
 }
 
+// The same per (head, row) work for the MFMA path, four heads of one row per workgroup: wave w
+// takes head 4 x + w of row y (x = blockIdx.x < 8, so the four are all Q, all K or all V), lane l
+// its elements l, l + 64, l + 128 and l + 192. Both RoPE pairs (t, t ^ 128) are then within the
+// lane, and the head's sum of squares is four wave sums added in the order of ck_block_sum (wave k
+// there holds elements 64 k ..), so every output has chunk_qkv_heads_kernel's bits; no LDS and no
+// barrier. 8 x M workgroups instead of 32 x M.
+template <ScaleKind SK, int ZS>
+__global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads4_kernel(QkvParams p, int m0, int M,
+                                                                    const float* __restrict__ part, int splits,
+                                                                    uint32_t* err) {
+    const int lane = threadIdx.x & 63, head = 4 * blockIdx.x + (threadIdx.x >> 6), m = blockIdx.y;
+    const int32_t rope_off = *p.rope_off, kv_off = *p.kv_off;
+    const int mm = m0 + m;
+    const bool rope_ok = rope_off >= 0 && (rope_off % (kDs * 2)) == 0 && rope_off / (kDs * 2) + mm < kE;
+    const bool kv_ok = kv_off >= 0 && (kv_off % (kNs * kDs * 2)) == 0 && kv_off / (kNs * kDs * 2) < kTs;
+    if (!rope_ok || !kv_ok) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, (rope_ok ? 0u : kErrRopeOffset) | (kv_ok ? 0u : kErrKvOffset));
+        return;
+    }
+    const int slot = (kv_off / (kNs * kDs * 2) + mm) % kTs;
+    const int trow = rope_off / (kDs * 2) + mm;
+    const float* prow = part + (size_t)m * kQkvRowsTotal + head * kDs + lane;
+    float pz[4][ZS];  // all partial loads in flight at once (split index clamped)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int z = 0; z < ZS; ++z) pz[k][z] = prow[(size_t)min(z, splits - 1) * M * kQkvRowsTotal + 64 * k];
+    const uint16_t* wn = head < 16 ? p.q_rms : (head < 24 ? p.k_rms : nullptr);
+    float v[4], ss[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int col = head * kDs + 64 * k + lane;
+        float acc = pz[k][0];
+#pragma unroll
+        for (int z = 1; z < ZS; ++z) acc = z < splits ? acc + pz[k][z] : acc;
+        const float sc = head < 16 ? chunk_scale<SK>(p.qs, col)
+                                   : (head < 24 ? chunk_scale<SK>(p.ks, col - kQs) : chunk_scale<SK>(p.vs, col - kQs - kPs));
+        v[k] = rbf(acc * sc);
+        ss[k] = wave_sum(v[k] * v[k]);
+    }
+    const float inv = rms_inverse(((ss[0] + ss[1]) + ss[2]) + ss[3], kDs);
+    float n[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float x = v[k] * inv;
+        if (wn) x = x * bf2f(wn[64 * k + lane]);
+        n[k] = rbf(x);
+    }
+    if (head >= 24) {
+        uint16_t* vd = p.v_cache + (size_t)slot * (kNs * kDs) + (head - 24) * kDs + lane;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) vd[64 * k] = (uint16_t)f2bf(n[k]);
+        return;
+    }
+    // the table's sin has its low half negated (generate_references.py:200-210): plain half swap
+    uint16_t* dst = (head < 16 ? p.q_out + (size_t)mm * kQs + head * kDs
+                               : p.k_cache + (size_t)slot * (kNs * kDs) + (head - 16) * kDs) + lane;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int t = 64 * k + lane;
+        const float cv = bf2f(p.cos[(size_t)trow * kDs + t]);
+        const float sv = bf2f(p.sin[(size_t)trow * kDs + t]);
+        dst[64 * k] = (uint16_t)f2bf(rbf(n[k] * cv) + rbf(n[k ^ 2] * sv));
+    }
+}
+
 // Per row: d = bf16((sum of the split-K partials) * s[n]), then out = bf16(bf16(r + N(d)) * ls)
 // with N the post-RMSNorm (identity when w_post is null) and ls skipped when null
 // (shared/rmsnorm.rs:204-296, residual.rs:189-241; generate_references.py:411-413).
@@ -739,15 +805,19 @@ hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, De
                                (size_t)M * kQkvRowsTotal);
     e = narrow ? gemm_partial<FfnFormat::FP8, kCkOBN>(g, sp, p.scale_kind, s) : gemm_partial(g, sp, p.scale_kind, s);
     if (e != hipSuccess) return e;
-    if (sp <= 2) return launch_qkv_heads(p, m0, M, ctx->fbuf, sp, s, ctx);
     const float* part = ctx->fbuf;
-    if (sp <= 4)  // as many partial loads in flight as there are splits
+    if (sp > 4) return hipErrorInvalidValue;  // 60 k steps: pick_splits never gives 8
+    // Up to 256 rows, one workgroup per (head, row): more workgroups hide the loads better (four
+    // heads per workgroup measured 28.5 -> 30.6 us for the call at M = 100, even at 256); beyond,
+    // four heads per workgroup (M = 1024: 101.5 -> 94.1 us).
+    if (narrow) return launch_qkv_heads(p, m0, M, part, sp, s, ctx);
+    if (sp <= 2)  // as many partial loads in flight as there are splits
         return p.scale_kind == ScaleKind::F32
-            ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32, 4>, dim3(32, M), s, p, m0, M, part, sp, ctx->err)
-            : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16, 4>, dim3(32, M), s, p, m0, M, part, sp, ctx->err);
+            ? ck_launch(chunk_qkv_heads4_kernel<ScaleKind::F32, 2>, dim3(8, M), s, p, m0, M, part, sp, ctx->err)
+            : ck_launch(chunk_qkv_heads4_kernel<ScaleKind::BF16, 2>, dim3(8, M), s, p, m0, M, part, sp, ctx->err);
     return p.scale_kind == ScaleKind::F32
-        ? ck_launch(chunk_qkv_heads_kernel<ScaleKind::F32>, dim3(32, M), s, p, m0, M, part, sp, ctx->err)
-        : ck_launch(chunk_qkv_heads_kernel<ScaleKind::BF16>, dim3(32, M), s, p, m0, M, part, sp, ctx->err);
+        ? ck_launch(chunk_qkv_heads4_kernel<ScaleKind::F32, 4>, dim3(8, M), s, p, m0, M, part, sp, ctx->err)
+        : ck_launch(chunk_qkv_heads4_kernel<ScaleKind::BF16, 4>, dim3(8, M), s, p, m0, M, part, sp, ctx->err);
 }
 
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
