@@ -84,7 +84,7 @@ def test_ffn_fp8_mfma_rows_without_post_norm_and_scalar():
                 atol=FFN_ATOL)
 
 
-@pytest.mark.parametrize("M", [17, 64, 100, 256])
+@pytest.mark.parametrize("M", [17, 64, 100, 256, 300])
 def test_o_mfma_rows(M):
     need_gpu()
     say(f"o M{M} (MFMA path)")
@@ -92,7 +92,9 @@ def test_o_mfma_rows(M):
     gate(o_oracle(d), o_gpu(d), f"o M{M}")
 
 
-@pytest.mark.parametrize("M", [17, 100, 256])
+# 300 and 600 rows: past one 256-row block, the QKV heads run four per workgroup (two k splits at
+# 300 rows, none at 600), and rows past the last multiple of 64 keep their own tile producers.
+@pytest.mark.parametrize("M", [17, 100, 256, 300, 600])
 def test_qkv_mfma_rows(M):
     need_gpu()
     say(f"qkv M{M} (MFMA path)")
