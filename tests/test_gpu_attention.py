@@ -43,6 +43,16 @@ def test_rows_with_different_masks_in_one_call():
     gate(run_oracle(d), run_gpu(d), "attention M3")
 
 
+def test_call_of_twenty_rows():
+    """20 rows run as one full 16-row launch and one of 4 (each launch's counters per (row, head)),
+    with mask rows from a single valid slot (position 0) to the full window (positions >= 1023)."""
+    need_gpu()
+    pos = [0, 1, 31, 32, 500, 1022, 1023, 1024, 1500, 2047, 2048, 3000, 4095, 4096, 5000, 6000, 7000, 7500, 8000, 8191]
+    say("attention M=20 (launches of 16 and 4 rows)")
+    d = synth.cfg_attention(seed=9, M=20, pos=pos, q_std=0.5)
+    gate(run_oracle(d), run_gpu(d), "attention M20")
+
+
 def test_scattered_mask():
     need_gpu()
     say("attention: random 0/1 mask")
