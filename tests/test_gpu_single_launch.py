@@ -20,7 +20,7 @@ from test_gpu_qkv import run_gpu as qkv_gpu
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("M", [17, 64, 100, 256])
+@pytest.mark.parametrize("M", [17, 64, 100, 256, 300])
 def test_ffn_fp8_mfma_rows(M):
     need_gpu()
     say(f"ffn fp8 M{M} (MFMA path)")
@@ -37,7 +37,7 @@ def fp4_case(fmt: str, M: int, tag: str = "mfma") -> dict:
     return dict(_fp4[fmt], residual=synth.bf16_normal(f"{tag}.{fmt}.M{M}.residual", (M, 3840)))
 
 
-@pytest.mark.parametrize("M", [17, 64, 256])
+@pytest.mark.parametrize("M", [17, 64, 256, 300])
 @pytest.mark.parametrize("fmt", ["mxfp4", "nvfp4"])
 def test_ffn_fp4_mfma_rows(fmt, M):
     """FP4 weights on the MFMA path: E2M1 codes widened with their block scales while they are
