@@ -167,6 +167,9 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
 /* ops::final_norm_and_logits -- FO/src/ops.rs:241-298 (oracle gemma4.py:256-261).
  * input bf16 [M,3840]; rms_weight bf16 [3840]; lm_head_weight bf16 [262144,3840]; out bf16
  * [M,262144] = bf16(tanh(l / 30) * 30) in f32, l = bf16(RMSNorm(input) . W_v). */
+int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight, const uint16_t* lm_head_weight,
+                              uint16_t* out, int M, void* stream);
+
 /* ---- full-attention layers (every sixth layer): 16 query heads and one KV head of 512, a
  * cache of 512-slot pages (FO/src/axes.rs: Gf=16, Df=512, Qf=8192, Pf=512, Tf=512). ---- */
 
@@ -210,9 +213,6 @@ int moa_full_attention(const uint16_t* q, const uint16_t* k_pages, const uint16_
 int moa_full_attention_output(const uint16_t* x, const float* running_sum, const uint16_t* post_attn_rms_weight,
                               const uint8_t* o_weight, const uint16_t* o_weight_scale, uint16_t* residual, int M,
                               void* stream);
-
-int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight, const uint16_t* lm_head_weight,
-                              uint16_t* out, int M, void* stream);
 
 /* The FP8 projection alone -- FO/scripts/generate_references.py:265-274 scaled_projection:
  * out[m,n] = bf16((x[m,:] . dec(w[n,:])) * scale[n]). x bf16 [M,K], w E4M3 [N,K], scale f32
