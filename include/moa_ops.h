@@ -13,6 +13,8 @@
  *   - stream is a hipStream_t (NULL = the null stream); all work is ordered on it and the
  *     call returns without synchronising. Calls on one device must be issued from one
  *     stream at a time: the per-device scratch is shared.
+ *   - the call is served by the scratch of the calling thread's current device (hipSetDevice),
+ *     so the stream and every tensor must belong to that device.
  * Pointers must be 16-byte aligned except per-channel scales (natural alignment) and FP4
  * block-scale codes (4-byte aligned).
  *

@@ -48,8 +48,15 @@ _I32 = (torch.int32,)
 
 
 def _stream(t: torch.Tensor) -> int:
-    """The current HIP stream of the tensor's device (its handle as an int)."""
-    return torch.cuda.current_stream(t.get_device()).cuda_stream
+    """The current HIP stream of the current device (its handle as an int). The library serves a
+    call from the scratch of the current device, so the call's tensors must live there: a tensor
+    of another device is refused here rather than run against the wrong device's scratch."""
+    dev = t.get_device()
+    cur = torch.cuda.current_device()
+    if dev != cur:
+        raise ValueError(f"the call's tensors live on cuda:{dev} but the current device is cuda:{cur}; "
+                         f"call it under torch.cuda.device({dev})")
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 def _rows(x: torch.Tensor, width: int, name: str) -> int:
@@ -252,10 +259,12 @@ def fp8_scaled_projection(x, w, scale, out) -> None:
 
 
 def device_errors(device: torch.device | None = None) -> int:
-    """Synchronise the current stream; return and clear the kernel-raised error bits."""
+    """Synchronise the current stream of `device` (default: the current device); return and clear
+    that device's kernel-raised error bits."""
     bits = C.c_uint32(0)
-    s = torch.cuda.current_stream(device).cuda_stream
-    _lib.call("moa_device_errors", C.c_void_p(s), C.byref(bits))
+    with torch.cuda.device(device):  # the library reads the bits of the current device
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call("moa_device_errors", C.c_void_p(s), C.byref(bits))
     return int(bits.value)
 
 
