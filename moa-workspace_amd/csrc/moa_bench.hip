@@ -16,9 +16,10 @@ namespace {
 
 // Workgroup b reads bytes [b * chunk, (b + 1) * chunk) of src (the last one up to n16), each wave
 // 1 KB per load instruction (16 contiguous bytes per lane), eight loads in flight per lane,
-// non-temporal, as the weight streams of the decode kernels read their rows. The XOR of all words
-// is stored only when it equals a value no input here produces, so the loads cannot be removed
-// and nothing is written.
+// non-temporal, as the weight streams of the decode kernels read their rows. A slice that ends
+// inside a batch of eight still issues that batch at once (the loads past the end are masked off),
+// so no shape degrades to one load in flight. The XOR of all words is stored only when it equals
+// a value no input here produces, so the loads cannot be removed and nothing is written.
 constexpr int kUnroll = 8;
 
 __global__ void stream_read_kernel(const uint4* __restrict__ src, uint64_t n16, uint32_t* sink) {
@@ -27,17 +28,15 @@ __global__ void stream_read_kernel(const uint4* __restrict__ src, uint64_t n16, 
     const uint64_t end = begin + chunk < n16 ? begin + chunk : n16;
     uint32_t acc = 0;
     const uint64_t step = (uint64_t)blockDim.x * kUnroll;
-    uint64_t i = begin + threadIdx.x;
-    for (; i + (kUnroll - 1) * blockDim.x < end; i += step) {
+    for (uint64_t i = begin + threadIdx.x; i < end; i += step) {
         uint4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) v[u] = ld_stream(src + i + (uint64_t)u * blockDim.x);
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t j = i + (uint64_t)u * blockDim.x;
+            v[u] = j < end ? ld_stream(src + j) : make_uint4(0, 0, 0, 0);
+        }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-    }
-    for (; i < end; i += blockDim.x) {
-        const uint4 v = ld_stream(src + i);
-        acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
