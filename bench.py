@@ -31,6 +31,8 @@ restatement of the reference's algorithm) on this host's cores for a bounded sam
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 10]
     python bench.py --profile ffn|o|qkv [--steps 20]
+    python bench.py --floor-shapes          # stream-read floor at several launch shapes
+    python bench.py --vendor-gemm           # torch.matmul on the config-4 GEMM shapes
 
 --profile runs one operator host-driven (one launch per call, no graph) over the rotating weight
 copies, then one device-to-device copy of 256 MiB: the fixed workload the rocprofv3 counter runs
@@ -104,6 +106,9 @@ def main() -> int:
                              "chunk", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
+    ap.add_argument("--floor-shapes", action="store_true",
+                    help="only time the stream-read kernel graph-replayed at several launch shapes (an empty "
+                         "launch and pure reads of O's and QKV's weight bytes); prints one JSON line")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only time torch.matmul (the vendor bf16 GEMM) on the chunk's four GEMM shapes with "
                          "bf16 weights, as a reference point for the MFMA path; prints one JSON line")
@@ -122,6 +127,10 @@ def main() -> int:
 
     torch.cuda.set_device(0)
     ops.init(0)
+    if args.floor_shapes:
+        sweep = floor_measure(torch, np, sweep=True)["sweep"]
+        print(json.dumps({"floor_shapes_us": sweep, "timing": "graph-replayed, median over replays, launch included"}))
+        return 0
     t0 = time.time()
     ffn = synth.cfg_ffn_fp8(0)
     o = synth.cfg_o(0)
@@ -497,11 +506,15 @@ def ckpt_measure(gib: float = 1.0):
     return {"GBps": round(gbps, 1), "pinned_copy_GBps": round(link, 1), "bytes": nbytes}
 
 
-def floor_measure(torch, np):
+FLOOR_SWEEP_SHAPES = ((240, 256), (240, 512), (256, 256), (256, 576), (256, 1024))
+
+
+def floor_measure(torch, np, sweep: bool = False):
     """The library's stream-read kernel (moa_bench_stream_read): the device's attainable read rate
     (1 GiB per launch, best of three launch shapes), and per one-token operator an empty launch and
     a pure read of its weight bytes at its launch shape, the windows rotated over 1 GiB so no
-    launch reads from the MALL. Graph-replayed like the operators."""
+    launch reads from the MALL. Graph-replayed like the operators. With sweep, only the empty
+    launch and the reads of O's and QKV's bytes at each of FLOOR_SWEEP_SHAPES (out["sweep"])."""
     import ctypes as C
 
     from moa_amd import _lib
@@ -537,6 +550,15 @@ def floor_measure(torch, np):
         per = np.array([ev[r].elapsed_time(ev[r + 1]) / calls for r in range(REPLAYS)])
         return float(np.median(per)) * 1e3  # us
 
+    if sweep:
+        table = {}
+        for label, nbytes in (("empty", 0), ("o", WEIGHT_BYTES["o"]), ("qkv", WEIGHT_BYTES["qkv"])):
+            for shape in FLOOR_SWEEP_SHAPES:
+                us = stats(read(nbytes, shape))
+                table[f"{label} {shape[0]}x{shape[1]}"] = round(us, 3)
+                log(f"floor sweep {label:5} {shape}: {us:.2f} us")
+        del buf
+        return {"sweep": table}
     out = {"attainable_shapes": {}}
     for shape in ((1024, 512), (512, 1024), (2048, 256)):
         us = stats(read(buf.numel(), shape, rotate=False), calls=8)
