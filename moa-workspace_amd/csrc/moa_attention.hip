@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kAtBlock) void attn_split_kernel(const uint16_t* __
     // factors exp(max_c - max) and the head's sum. Every thread reads dims 4 q .. 4 q + 3
     // (q = t % 64) of chunks 8 (t / 64) .. + 7 for both heads as 16-byte loads, all issued before
     // any is used; the four chunk groups then meet in LDS in a fixed order. Partials are read
-    // coherently (agent scope: buffer loads with sc1, scalar atomic loads).
+    // coherently (agent scope: 16-byte buffer loads with sc1, and per-thread one-float atomic loads).
     __shared__ float sf[kGs][kAtChunks], sl[kGs];
     __shared__ float4 so[4][kGs][kDs / 4];
     const float* hp = part + ((size_t)m * kNs + n) * kAtChunks * kGs * kAtPartFloats;
