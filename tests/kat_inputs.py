@@ -257,6 +257,80 @@ def ffn_stress_inputs() -> dict:
     return out
 
 
+def ffn_stress_inputs_fp8() -> dict:
+    """The full-FFN stress construction (full-ffn-stress/generate_reference.py:34-92) restated for
+    E4M3 weights with per-row f32 scales. Every projection reproduces the NVFP4 case's values:
+    ordinary up/gate rows 2^-11 / 2^-10, rows 0 and 7680 up 32 / 2^-4 and gate 32 / 8, so the
+    GeGLU row is p[0] = 1024, p[7680] = 0.5 and 2^-22 elsewhere; the down rows skip columns 0 and
+    7680 (the large p) and sum 7679 x 2^-22 x 90 x 2^-11 = 691110 x 2^-33, whose bf16 is
+    169 x 2^-21, the NVFP4 case's d. Rows 0 and 7680 and the odd down rows carry other scales
+    than their neighbours (their codes compensate), so a row-scale index error changes the
+    answer. Expected output: 3840 x 0x3ecf, the reference's recorded answer."""
+    ones = np.full(H, 0x3F80, np.uint16)
+    out = dict(residual=ones.copy(), pre_ff_rms_weight=ones.copy(), post_ff_rms_weight=ones.copy(),
+               layer_scalar=np.full(8, 0x3EC0, np.uint16))
+    E4 = {1.0: 0x38, 2.0: 0x40, 3.0: 0x44}
+    for name, big_row in (("up", 5), ("gate", 682)):
+        codes = np.zeros((L, H), np.uint8)
+        scale = np.full(L, 2.0 ** -11, np.float32)
+        codes[:, 0] = E4[1.0] if name == "up" else E4[2.0]
+        # rows 0 and 7680 at scale 2^-8: 2730 x 3 + 2 = 8192 -> 32; 5 x 3 + 1 = 16 -> 2^-4 (up);
+        # 682 x 3 + 2 = 2048 -> 8 (gate)
+        codes[0, :] = 0
+        codes[0, :2730] = E4[3.0]
+        codes[0, 2730] = E4[2.0]
+        codes[7680, :] = 0
+        codes[7680, :big_row] = E4[3.0]
+        codes[7680, big_row] = E4[1.0] if name == "up" else E4[2.0]
+        scale[[0, 7680]] = 2.0 ** -8
+        out[f"{name}_weight"], out[f"{name}_weight_scale"] = codes, scale
+    codes = np.zeros((H, L), np.uint8)
+    codes[:1920, 1:7680] = E4[1.0]
+    codes[1920:, 7681:] = E4[1.0]
+    scale = np.full(H, 90 * 2.0 ** -11, np.float32)
+    codes[1::2][codes[1::2] != 0] = E4[2.0]  # odd rows: weight 2, scale 45 x 2^-11
+    scale[1::2] = 45 * 2.0 ** -11
+    out["down_weight"], out["down_weight_scale"] = codes, scale
+    return out
+
+
+def ffn_stress_inputs_mxfp4() -> dict:
+    """The full-FFN stress construction restated for E2M1 weights with E8M0 block-32 scales (no
+    global scale: proj = bf16(h . W)). Same intermediates as the NVFP4 case (see
+    ffn_stress_inputs_fp8). Rows 0 and 7680 of up/gate alternate their block scales 2^-9 / 2^-8
+    with codes 6 / 3, so every element is 3 x 2^-8 whichever block it is in; the down rows take
+    block scales 2^-7, 2^-6, 2^-5 in turn, each element 3/64 (6274 columns) or 1/32 (1405),
+    which sums to exactly 338 x 2^-22 = 169 x 2^-21. A wrong block index or E8M0 bias changes the
+    answer. Expected output: 3840 x 0x3ecf."""
+    ones = np.full(H, 0x3F80, np.uint16)
+    out = dict(residual=ones.copy(), pre_ff_rms_weight=ones.copy(), post_ff_rms_weight=ones.copy(),
+               layer_scalar=np.full(8, 0x3EC0, np.uint16))
+    pack = lambda c: (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+    for name in ("up", "gate"):
+        codes = np.zeros((L, H), np.uint8)
+        sc = (127 + (np.arange(H // 32) % 5)[None, :] + np.zeros((L, 1), np.int64)).astype(np.uint8)
+        codes[:, 0] = 1 if name == "up" else 2  # 0.5 / 1.0 x 2^-10
+        sc[:, 0] = 127 - 10
+        for row, n in ((0, 2730), (7680, 5 if name == "up" else 682)):
+            codes[row, :] = 0
+            blk = np.arange(H) // 32
+            sc[row] = np.where(np.arange(H // 32) % 2 == 0, 127 - 9, 127 - 8)
+            codes[row, :n] = np.where(blk[:n] % 2 == 0, 7, 5)  # 6 x 2^-9 = 3 x 2^-8
+            # the last element: 2^-7 (to 32 / 8) or, up row 7680 (block 0, 2^-9), 2^-8 (to 2^-4)
+            codes[row, n] = 4  # 2.0 x the block's scale
+        out[f"{name}_weight_packed"], out[f"{name}_weight_scale"] = pack(codes), sc
+    codes = np.zeros((H, L), np.uint8)
+    e = np.arange(L // 32) % 3  # block scale 2^(-7 + e)
+    big, small = np.array([7, 5, 3])[e], np.array([6, 4, 2])[e]  # 3/64 and 1/32 at each scale
+    col_blk = np.arange(L) // 32
+    for rows, c0 in ((slice(0, 1920), 1), (slice(1920, H), 7681)):
+        codes[rows, c0:c0 + 6274] = big[col_blk[c0:c0 + 6274]]
+        codes[rows, c0 + 6274:c0 + 7679] = small[col_blk[c0 + 6274:c0 + 7679]]
+    out["down_weight_packed"] = pack(codes)
+    out["down_weight_scale"] = np.broadcast_to((127 - 7 + e).astype(np.uint8), (H, L // 32)).copy()
+    return out
+
+
 def sign_failures(expected_f32: np.ndarray, actual_f32: np.ndarray, atol: float) -> np.ndarray:
     """BASELINE's "no sign-cancellation failures": where the expected value is at least atol in
     magnitude, the output must carry its sign. (The atol/rtol bound alone lets an output flip sign

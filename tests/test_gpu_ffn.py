@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 from gpu_util import dev, gate, gate_addend, host, need_gpu, say, torch
-from kat_inputs import GOLDEN, ffn_stress_inputs, unbf
+from kat_inputs import GOLDEN, ffn_stress_inputs, ffn_stress_inputs_fp8, ffn_stress_inputs_mxfp4, unbf
 from moa_amd import prng, synth
 from oracle import oracle as O
 
@@ -76,6 +76,20 @@ def test_nvfp4_stress_known_answer():
     got = gpu_nvfp4(ffn_stress_inputs())
     want = np.fromfile(GOLDEN / "ffn_stress_expected_bf16.bin", dtype="<u2")
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M", [1, 16, 256])
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+def test_stress_known_answer_other_formats(fmt, M):
+    """The FP8 and MXFP4 restatements of full-ffn-stress (the same intermediates, closed-form
+    answer 3840 x 0x3ecf, pinned on the oracle in test_oracle_ffn_formats.py) through the
+    one-token kernel (M = 1), the rows kernels (M = 16) and the MFMA chunk path (M = 256)."""
+    need_gpu()
+    say(f"ffn {fmt} stress M{M}")
+    d = ffn_stress_inputs_fp8() if fmt == "fp8" else ffn_stress_inputs_mxfp4()
+    d["residual"] = np.broadcast_to(d["residual"], (M, 3840)).copy()
+    got = (gpu_fp8 if fmt == "fp8" else gpu_mxfp4)(d)
+    assert np.all(np.asarray(got).reshape(-1) == 0x3ECF), np.unique(got)
 
 
 @pytest.mark.parametrize("run", range(9))
