@@ -58,12 +58,15 @@ const char* moa_version(void);
 /* Reason for the last non-zero return on this thread. */
 const char* moa_last_error_string(void);
 
-/* Allocates the per-device scratch of `device` (also done lazily by the first call). Call it
- * before capturing calls into a HIP graph. */
+/* Allocates the per-device scratch of `device` (also done lazily by the first call) and sets up
+ * the static scratch of moa_decoder_feedforward_fp8_noalloc. Call it before capturing calls into
+ * a HIP graph. A caller that cannot allocate skips it: the no-allocation entry point sets itself
+ * up on its first call without allocating. */
 int moa_init(int device);
 
 /* Synchronises `stream`, returns the OR of device-side error bits raised since the last call
- * (MOA_DEVERR_*) in *bits, and clears them. */
+ * (MOA_DEVERR_*) in *bits, and clears them. Reads the error word of each scratch that exists on
+ * the current device and creates none, so it allocates nothing. */
 int moa_device_errors(void* stream, uint32_t* bits);
 
 /* ops::sliding_project_qkv -- FO/src/ops.rs:37-76.
@@ -145,8 +148,8 @@ int moa_decoder_feedforward_fp8(uint16_t* residual, const uint16_t* pre_ff_rms_w
  * moa_decoder_feedforward_fp8, the same kernels and the same bits, for 1 <= M <= 16 rows (larger
  * M is rejected with MOA_ERROR_INVALID_VALUE). Its scratch (about 1.9 MB: epoch counters,
  * hand-off words, normalised rows, GeGLU rows, down partial sums) is a static device array that
- * each GPU holds until the process ends; neither this call nor its set-up (first call on a
- * device, or moa_init) allocates. Every call on one device shares that array and it keeps the
+ * each GPU holds until the process ends; neither this call nor its set-up (done by its first
+ * call on a device) allocates, and moa_device_errors reads its error bits without allocating. Every call on one device shares that array and it keeps the
  * last call's contents: calls that overlap on one device (different streams, no dependency)
  * race. Independent of the scratch of the other entry points. */
 int moa_decoder_feedforward_fp8_noalloc(uint16_t* residual, const uint16_t* pre_ff_rms_weight,
@@ -252,8 +255,14 @@ int moa_test_preset_epochs(uint64_t launches);
 int moa_test_set_stall(uint32_t steal_ticks, uint32_t hold_ticks, const int32_t* hold);
 
 /* Test support: the number of take-overs (a wait that did another workgroup's share) on the
- * current device since the last call, then resets it. Synchronises the device. */
+ * current device since the last call, in the scratch of every entry point that has run there
+ * (the no-allocation entry point's included), then resets it. Synchronises the device. */
 int moa_test_take_overs(uint32_t* count);
+
+/* Test support: which scratch exists on the current device, without creating either: bit 0 the
+ * hipMalloc'd scratch of the ordinary entry points, bit 1 the static scratch of
+ * moa_decoder_feedforward_fp8_noalloc. Touches no device memory. */
+int moa_test_scratch_state(uint32_t* state);
 
 #ifdef __cplusplus
 }

@@ -46,22 +46,29 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 def build(verbose: bool = False) -> Path:
     """Compiles every source to an object (in parallel: the translation units are independent),
-    then links the shared library."""
+    then links the shared library. Objects and the linked file go to a directory of this build's
+    own, so builds that run at the same time never read each other's half-written files; the
+    library is then replaced in one step."""
+    import shutil
+    import tempfile
     from concurrent.futures import ThreadPoolExecutor
 
     srcs = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
-    objdir = PKG / "_build"
-    objdir.mkdir(exist_ok=True)
-    objs = [objdir / (s.stem + ".o") for s in srcs]
-    compile_flags = [f for f in FLAGS if f != "-shared"]
-    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
-    with ThreadPoolExecutor(jobs) as ex:
-        for f in [ex.submit(_run, [HIPCC, *compile_flags, "-c", "-o", str(o), str(s)], verbose)
-                  for s, o in zip(srcs, objs)]:
-            f.result()
-    tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
-    os.replace(tmp, LIB)
+    (PKG / "_build").mkdir(exist_ok=True)
+    objdir = Path(tempfile.mkdtemp(prefix="build-", dir=PKG / "_build"))
+    try:
+        objs = [objdir / (s.stem + ".o") for s in srcs]
+        compile_flags = [f for f in FLAGS if f != "-shared"]
+        jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+        with ThreadPoolExecutor(jobs) as ex:
+            for f in [ex.submit(_run, [HIPCC, *compile_flags, "-c", "-o", str(o), str(s)], verbose)
+                      for s, o in zip(srcs, objs)]:
+                f.result()
+        tmp = objdir / LIB.name
+        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+        os.replace(tmp, LIB)
+    finally:
+        shutil.rmtree(objdir, ignore_errors=True)
     return LIB
 
 

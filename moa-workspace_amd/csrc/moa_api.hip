@@ -34,6 +34,11 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int set_error(int code, const char* msg) { return fail(code, msg); }
 
+DevCtx* existing_context(int dev) {
+    std::lock_guard<std::mutex> lock(g_ctx_mutex);
+    return g_ctx[dev].base ? &g_ctx[dev] : nullptr;
+}
+
 DevCtx* device_context(hipError_t* err) {
     int dev = 0;
     *err = hipGetDevice(&dev);
@@ -297,21 +302,25 @@ int moa_init(int device) {
 
 int moa_device_errors(void* stream, uint32_t* bits) {
     if (!bits) return fail(MOA_ERROR_INVALID_VALUE, "bits is NULL");
-    int code = MOA_SUCCESS;
-    DevCtx* ctx = ctx_or_fail(&code);
-    if (!ctx) return code;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(MOA_ERROR_NO_DEVICE, "device index out of range");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // the no-allocation entry point's error word too, once its scratch is set up on this device
-    const DevCtx* na = nullptr;
+    // The error words of whichever scratch exists on this device: the hipMalloc'd one of the
+    // other entry points and the static one of the no-allocation entry point. Neither is created
+    // here, so a caller that cannot allocate reads its calls' errors without allocating.
+    const DevCtx* ctxs[2] = {existing_context(dev), nullptr};
     {
         std::lock_guard<std::mutex> lock(g_na_mutex);
-        if (g_na_ctx[ctx->device].base) na = &g_na_ctx[ctx->device];
+        if (g_na_ctx[dev].base) ctxs[1] = &g_na_ctx[dev];
     }
     uint32_t host[2] = {0, 0};
-    hipError_t e = hipMemcpyAsync(&host[0], ctx->err, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipMemsetAsync(ctx->err, 0, sizeof(uint32_t), s);
-    if (e == hipSuccess && na) e = hipMemcpyAsync(&host[1], na->err, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess && na) e = hipMemsetAsync(na->err, 0, sizeof(uint32_t), s);
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        if (!ctxs[i]) continue;
+        e = hipMemcpyAsync(&host[i], ctxs[i]->err, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipMemsetAsync(ctxs[i]->err, 0, sizeof(uint32_t), s);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "reading device error bits");
     *bits = host[0] | host[1];
@@ -571,14 +580,45 @@ int moa_test_take_overs(uint32_t* count) {
     Check c;
     c.ptr(count, "count", 1);
     if (c.code) return c.code;
-    int code = MOA_SUCCESS;
-    DevCtx* ctx = ctx_or_fail(&code);
-    if (!ctx) return code;
-    hipError_t e = hipDeviceSynchronize();
-    if (e == hipSuccess) e = hipMemcpy(count, ctx->err + kErrTakeOvers, sizeof(uint32_t), hipMemcpyDeviceToHost);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(MOA_ERROR_NO_DEVICE, "device index out of range");
+    // both scratches' counters, as moa_device_errors reads both error words
+    const DevCtx* ctxs[2] = {existing_context(dev), nullptr};
+    {
+        std::lock_guard<std::mutex> lock(g_na_mutex);
+        if (g_na_ctx[dev].base) ctxs[1] = &g_na_ctx[dev];
+    }
+    e = hipDeviceSynchronize();
+    uint32_t total = 0;
     const uint32_t zero = 0;
-    if (e == hipSuccess) e = hipMemcpy(ctx->err + kErrTakeOvers, &zero, sizeof zero, hipMemcpyHostToDevice);
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        if (!ctxs[i]) continue;
+        uint32_t n = 0;
+        e = hipMemcpy(&n, ctxs[i]->err + kErrTakeOvers, sizeof n, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(ctxs[i]->err + kErrTakeOvers, &zero, sizeof zero, hipMemcpyHostToDevice);
+        total += n;
+    }
+    if (e == hipSuccess) *count = total;
     return finish(e, "reading the take-over count");
+}
+
+int moa_test_scratch_state(uint32_t* state) {
+    Check c;
+    c.ptr(state, "state", 4);
+    if (c.code) return c.code;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(MOA_ERROR_NO_DEVICE, "device index out of range");
+    uint32_t v = existing_context(dev) ? 1u : 0u;
+    {
+        std::lock_guard<std::mutex> lock(g_na_mutex);
+        if (g_na_ctx[dev].base) v |= 2u;
+    }
+    *state = v;
+    return MOA_SUCCESS;
 }
 
 int moa_format_selftest(uint32_t* out, void* stream) {

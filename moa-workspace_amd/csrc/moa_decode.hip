@@ -14,6 +14,7 @@
 //     last-arriving wave, found with a device-scope ticket -- no second launch.
 // blockIdx.y indexes the token row (M <= kMaxDecodeM); rows re-read the same weights, which
 // for small M mostly hit L2/MALL.
+#include <mutex>
 #include <utility>
 
 #include "moa_device.h"
@@ -1763,16 +1764,27 @@ template <typename K>
 static bool fits_resident(int8_t& known, K kernel, int block, int grid, const DevCtx* ctx);
 
 // The waits' take-over threshold (and, in tests, held workgroups) passed to every single-launch
-// kernel.
+// kernel. A test may change it from any thread while another launches: the mutex makes each
+// launch copy one whole Stall.
 static Stall g_stall = {kStealTicks, 0, {-1, -1, -1, -1}};
+static std::mutex g_stall_mutex;
 
-void set_stall(const Stall& st) { g_stall = st; }
+void set_stall(const Stall& st) {
+    std::lock_guard<std::mutex> lock(g_stall_mutex);
+    g_stall = st;
+}
+
+static Stall current_stall() {
+    std::lock_guard<std::mutex> lock(g_stall_mutex);
+    return g_stall;
+}
 
 // A single-launch kernel, or its Hold instantiation while a test holds workgroups.
 template <typename K, typename KH, typename... A>
 static hipError_t launch_fused(K kernel, KH kernel_hold, dim3 grid, int block, hipStream_t s, A... args) {
-    if (g_stall.hold_ticks) hipLaunchKernelGGL(kernel_hold, grid, dim3(block), 0, s, args..., g_stall);
-    else hipLaunchKernelGGL(kernel, grid, dim3(block), 0, s, args..., g_stall);
+    const Stall st = current_stall();
+    if (st.hold_ticks) hipLaunchKernelGGL(kernel_hold, grid, dim3(block), 0, s, args..., st);
+    else hipLaunchKernelGGL(kernel, grid, dim3(block), 0, s, args..., st);
     return hipGetLastError();
 }
 

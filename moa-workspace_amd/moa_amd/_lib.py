@@ -78,6 +78,7 @@ SIGNATURES = {
     "moa_test_preset_epochs": [U64],
     "moa_test_set_stall": [C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)],
     "moa_test_take_overs": [U32P],
+    "moa_test_scratch_state": [U32P],
     # include/moa_bench.h
     "moa_bench_stream_read": [P, U64, I32, I32, P, P],
 }

@@ -3,7 +3,7 @@ on the GPU vs the CPU oracle and the reference's known answer."""
 import numpy as np
 import pytest
 
-from gpu_util import dev, gate, gate_addend, host, need_gpu, say, torch
+from gpu_util import dev, gate, host, need_gpu, say, torch
 from kat_inputs import GOLDEN, ffn_stress_inputs, ffn_stress_inputs_fp8, ffn_stress_inputs_mxfp4, unbf
 from moa_amd import prng, synth
 from oracle import oracle as O
@@ -119,8 +119,7 @@ def test_fp8_config0(seed, cfg0):
 def test_fp8_config0_literal_without_post_norm_and_gate(cfg0):
     """BASELINE config 0 read literally: pre-RMSNorm -> GeGLU -> down -> residual add."""
     need_gpu()
-    gate_addend(oracle_fp8(cfg0, False, False), gpu_fp8(cfg0, False, False), cfg0["residual"], "ffn fp8 cfg0 literal",
-                atol=FFN_ATOL)
+    gate(oracle_fp8(cfg0, False, False), gpu_fp8(cfg0, False, False), "ffn fp8 cfg0 literal", atol=FFN_ATOL)
 
 
 def test_fp8_multi_row_and_determinism():

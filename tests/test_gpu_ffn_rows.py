@@ -7,7 +7,7 @@ rows."""
 import numpy as np
 import pytest
 
-from gpu_util import gate, gate_addend, need_gpu, say
+from gpu_util import gate, need_gpu, say
 from moa_amd import synth
 from oracle import oracle as O
 from test_gpu_ffn import (FFN_ATOL, assert_geglu_near_zero, cancel_fp4_codes, cancellation_residual, gpu_fp8, gpu_mxfp4,
@@ -71,8 +71,7 @@ def test_rows_without_post_norm_and_layer_scalar():
     need_gpu()
     say("ffn rows fp8 M3 without post-norm and layer scalar")
     d = case("fp8", 3, "plain")
-    gate_addend(oracle_fp8(d, False, False), gpu_fp8(d, False, False), d["residual"], "ffn rows fp8 M3 plain",
-                atol=FFN_ATOL)
+    gate(oracle_fp8(d, False, False), gpu_fp8(d, False, False), "ffn rows fp8 M3 plain", atol=FFN_ATOL)
 
 
 @pytest.mark.parametrize("M", [4, 16])
