@@ -58,6 +58,9 @@ MALL_BYTES = 256 << 20
 # Algorithmic bytes per call (weights + scales + operator-boundary vectors).
 FATTN_PAGES = 8  # full-attention decode at position 4095: pages 0..7
 BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
+         # O then the FFN in one launch: both operators' bytes less the residual row between them,
+         # which never goes to memory (one 7,680-byte write and one read)
+         "o_ffn": 15_775_232 + 177_116_176 - 2 * 3840 * 2,
          # config 3, MXFP4 weights (E2M1 codes + E8M0 block-32 scales) at M = 1 and M = 16 rows: the
          # weights once, plus the rows' residual read and write, the two norm weights, the layer scalar
          "ffn_mxfp4": 94_003_200 + 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
@@ -102,7 +105,7 @@ def main() -> int:
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
-                                          "ffn_mxfp4", "ffn_mxfp4_m16",
+                                          "ffn_mxfp4", "ffn_mxfp4_m16", "o_ffn",
                              "chunk", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
@@ -260,6 +263,12 @@ def main() -> int:
         w = OW[i % no]
         ops.sliding_attention_output(o_x, o_post, w["o_weight"], w["o_weight_scale"], o_res)
 
+    def run_o_ffn(i):
+        v, w = OW[i % no], FW[i % nf]
+        ops.sliding_attention_output_feedforward_fp8(
+            o_x, o_post, v["o_weight"], v["o_weight_scale"], f_res, f_pre, w["up_weight"], w["gate_weight"],
+            w["down_weight"], w["up_weight_scale"], w["gate_weight_scale"], w["down_weight_scale"], f_post, f_ls)
+
     def run_qkv(i):
         w = QW[i % nq]
         ops.sliding_project_qkv(q["x"], w["q_weight"], w["k_weight"], w["v_weight"], w["q_weight_scale"],
@@ -302,6 +311,10 @@ def main() -> int:
         run_qkv(i)
         run_o(i)
         run_ffn(i)
+
+    def run_step_fused(i):
+        run_qkv(i)
+        run_o_ffn(i)
 
     def timed(fn, steps, warmup):
         """Host-driven: one library call per launch (includes Python/ctypes submission)."""
@@ -348,7 +361,7 @@ def main() -> int:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
               "fattn_fused64": run_fattn_fused64, "fo": run_fo, "ffn_mxfp4": run_ffn_mxfp4,
-              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer}[args.profile]
+              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer, "o_ffn": run_o_ffn}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -363,7 +376,7 @@ def main() -> int:
     floor = floor_measure(torch, np)
 
     per_op = {}
-    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
+    for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("o_ffn", run_o_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
                      ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("attn", run_attn), ("logits", run_logits),
                      ("fqkv", run_fqkv), ("fattn", run_fattn), ("fattn_fused", run_fattn_fused),
                      ("fattn_fused64", run_fattn_fused64), ("fo", run_fo)):
@@ -382,6 +395,9 @@ def main() -> int:
     ms_step_host = timed(run_step, min(args.steps, 50), 5)
     log(f"step {ms_step * 1e3:9.2f} us/token [p10 {step_p10 * 1e3:.2f}, p90 {step_p90 * 1e3:.2f}]   "
         f"(host-driven {ms_step_host * 1e3:.2f} us)")
+    # the same step with O and the FFN in one launch (moa_sliding_attention_output_feedforward_fp8)
+    ms_fstep, fstep_p10, fstep_p90 = graph_stats(run_step_fused, calls=args.steps, warmup=max(args.warmup, 1))
+    log(f"step, O->FFN fused {ms_fstep * 1e3:9.2f} us/token [p10 {fstep_p10 * 1e3:.2f}, p90 {fstep_p90 * 1e3:.2f}]")
 
     chunk = None
     if CM:
@@ -442,6 +458,10 @@ def main() -> int:
                      "algorithmic_bytes": BYTES["ffn"], "avg_us": f["us"], "traffic": traffic,
                      "traffic_source": "profiles/hbm_traffic_m1.md" if traffic else None},
         "ops": per_op,
+        "step_o_ffn_fused": {"us": round(ms_fstep * 1e3, 3), "us_p10": round(fstep_p10 * 1e3, 3),
+                             "us_p90": round(fstep_p90 * 1e3, 3),
+                             "workload": "sliding_project_qkv (cfg2) + sliding_attention_output_feedforward_fp8 "
+                                         "(cfg1 then cfg0, one launch)"},
         "floor": floor,
         "us_per_token_host_driven": round(ms_step_host * 1e3, 3),
         "hbm_copy_GBps": round(copy_gbps, 1),

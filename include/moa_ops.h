@@ -169,6 +169,40 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
                                   const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar,
                                   int M, void* stream);
 
+/* The tail of the reference's sliding-layer decode step, FO/src/host/runtime.rs:440-459 (the
+ * ops::sliding_attention_output launch) followed by 543-571 (the ops::decoder_feedforward launch of
+ * mlp) on the same residual: O projection, post-attention norm and residual add (FO/src/ops.rs:130-146),
+ * then the GeGLU FFN (FO/src/ops.rs:201-239), with the reference's operand types (bf16 O scales,
+ * NVFP4 FFN weights). Arguments are those of moa_sliding_attention_output_bf16_scales followed by
+ * those of moa_decoder_feedforward after its residual. The residual afterwards has the same bits
+ * as those two calls made in turn; at M = 1 it is one launch (the residual between the two
+ * operators is never written to memory). */
+int moa_sliding_attention_output_feedforward(
+    const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const uint16_t* o_weight_scale,
+    uint16_t* residual, const uint16_t* pre_ff_rms_weight, const uint8_t* up_weight_packed,
+    const uint8_t* gate_weight_packed, const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+    const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale, const float* up_global_scale,
+    const float* gate_global_scale, const float* down_global_scale, const uint16_t* post_ff_rms_weight,
+    const uint16_t* layer_scalar, int M, void* stream);
+
+/* The same with BASELINE's operand types: f32 O scales and the FP8 FFN of
+ * moa_decoder_feedforward_fp8 (post_ff_rms_weight and layer_scalar may be NULL). The same bits as
+ * moa_sliding_attention_output then moa_decoder_feedforward_fp8. */
+int moa_sliding_attention_output_feedforward_fp8(
+    const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const float* o_weight_scale,
+    uint16_t* residual, const uint16_t* pre_ff_rms_weight, const uint8_t* up_weight, const uint8_t* gate_weight,
+    const uint8_t* down_weight, const float* up_weight_scale, const float* gate_weight_scale,
+    const float* down_weight_scale, const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar, int M,
+    void* stream);
+
+/* The same with f32 O scales and the MXFP4 FFN of moa_decoder_feedforward_mxfp4. */
+int moa_sliding_attention_output_feedforward_mxfp4(
+    const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const float* o_weight_scale,
+    uint16_t* residual, const uint16_t* pre_ff_rms_weight, const uint8_t* up_weight_packed,
+    const uint8_t* gate_weight_packed, const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+    const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale, const uint16_t* post_ff_rms_weight,
+    const uint16_t* layer_scalar, int M, void* stream);
+
 /* ops::final_norm_and_logits -- FO/src/ops.rs:241-298 (oracle gemma4.py:256-261).
  * input bf16 [M,3840]; rms_weight bf16 [3840]; lm_head_weight bf16 [262144,3840]; out bf16
  * [M,262144] = bf16(tanh(l / 30) * 30) in f32, l = bf16(RMSNorm(input) . W_v). */

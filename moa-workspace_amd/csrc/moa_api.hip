@@ -60,6 +60,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_f = carve(sizeof(float) * kChunkPartFloats);
     const size_t t_part = carve(sizeof(uint64_t) * kFfnSlotWords);
     const size_t t_opart = carve(sizeof(uint64_t) * kFfnSlotWords);
+    const size_t t_ofnpart = carve(sizeof(uint64_t) * kFfnSlotWords * kOfnCopies);
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
     const size_t t_ptag = carve(sizeof(uint64_t) * (kL / 2));
     const size_t t_attn = carve(sizeof(float) * kAttnPartFloats);
@@ -87,6 +88,7 @@ DevCtx* device_context(hipError_t* err) {
     c.fbuf = reinterpret_cast<float*>(b + t_f);
     c.ffn_part = reinterpret_cast<uint64_t*>(b + t_part);
     c.o_part = reinterpret_cast<uint64_t*>(b + t_opart);
+    c.ofn_part = reinterpret_cast<uint64_t*>(b + t_ofnpart);
     c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
     c.ffn_ptag = reinterpret_cast<uint64_t*>(b + t_ptag);
     c.attn_part = reinterpret_cast<float*>(b + t_attn);
@@ -225,15 +227,14 @@ int qkv_common(const QkvParams& p, int M, void* stream) {
     return MOA_SUCCESS;
 }
 
-int o_common(const OParams& p, int M, void* stream) {
+int o_check(const OParams& p, int M) {
     Check c;
     c.ptr(p.x, "x").ptr(p.post_rms, "post_attn_rms_weight").ptr(p.ow, "o_weight");
     c.ptr(p.os, "o_weight_scale", p.scale_kind == ScaleKind::F32 ? 4 : 2).ptr(p.residual, "residual").rows(M);
-    if (c.code) return c.code;
-    int code = MOA_SUCCESS;
-    DevCtx* ctx = ctx_or_fail(&code);
-    if (!ctx) return code;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    return c.code;
+}
+
+int o_launch(const OParams& p, int M, hipStream_t s, DevCtx* ctx) {
     if (M <= kMaxDecodeM) return finish(launch_o_decode(p, M, s, ctx), "sliding_attention_output launch");
     for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
         const int e = finish(launch_o_chunk(p, m0, M - m0 < kMaxChunkM ? M - m0 : kMaxChunkM, s, ctx),
@@ -241,6 +242,14 @@ int o_common(const OParams& p, int M, void* stream) {
         if (e) return e;
     }
     return MOA_SUCCESS;
+}
+
+int o_common(const OParams& p, int M, void* stream) {
+    if (const int bad = o_check(p, M)) return bad;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return o_launch(p, M, static_cast<hipStream_t>(stream), ctx);
 }
 
 int ffn_check(const FfnParams& p, int M) {
@@ -264,12 +273,7 @@ int ffn_check(const FfnParams& p, int M) {
     return c.code;
 }
 
-int ffn_common(const FfnParams& p, int M, void* stream) {
-    if (const int bad = ffn_check(p, M)) return bad;
-    int code = MOA_SUCCESS;
-    DevCtx* ctx = ctx_or_fail(&code);
-    if (!ctx) return code;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+int ffn_launch(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx) {
     // More than kMaxDecodeM rows take the MFMA path (every weight format).
     if (M <= kMaxDecodeM) return finish(launch_ffn_decode(p, M, s, ctx), "decoder_feedforward launch");
     for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
@@ -278,6 +282,30 @@ int ffn_common(const FfnParams& p, int M, void* stream) {
         if (e) return e;
     }
     return MOA_SUCCESS;
+}
+
+int ffn_common(const FfnParams& p, int M, void* stream) {
+    if (const int bad = ffn_check(p, M)) return bad;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    return ffn_launch(p, M, static_cast<hipStream_t>(stream), ctx);
+}
+
+// sliding_attention_output then decoder_feedforward on one residual: one launch for a token row
+// when a single-launch kernel covers the operand types, else the two operators in turn.
+int o_ffn_common(const OParams& o, const FfnParams& p, int M, void* stream) {
+    if (const int bad = o_check(o, M)) return bad;
+    if (const int bad = ffn_check(p, M)) return bad;
+    int code = MOA_SUCCESS;
+    DevCtx* ctx = ctx_or_fail(&code);
+    if (!ctx) return code;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    if (M == 1 && launch_o_ffn_fused(o, p, s, ctx, &e))
+        return finish(e, "sliding_attention_output_feedforward launch");
+    if (const int bad = o_launch(o, M, s, ctx)) return bad;
+    return ffn_launch(p, M, s, ctx);
 }
 
 }  // namespace
@@ -420,6 +448,46 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
                 down_weight_packed, up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
                 nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
     return ffn_common(p, M, stream);
+}
+
+int moa_sliding_attention_output_feedforward(
+    const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const uint16_t* o_weight_scale,
+    uint16_t* residual, const uint16_t* pre_ff_rms_weight, const uint8_t* up_weight_packed,
+    const uint8_t* gate_weight_packed, const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+    const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale, const float* up_global_scale,
+    const float* gate_global_scale, const float* down_global_scale, const uint16_t* post_ff_rms_weight,
+    const uint16_t* layer_scalar, int M, void* stream) {
+    OParams o{x, post_attn_rms_weight, o_weight, o_weight_scale, ScaleKind::BF16, residual};
+    FfnParams p{FfnFormat::NVFP4, residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed,
+                down_weight_packed, up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                up_global_scale, gate_global_scale, down_global_scale, post_ff_rms_weight, layer_scalar};
+    return o_ffn_common(o, p, M, stream);
+}
+
+int moa_sliding_attention_output_feedforward_fp8(
+    const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const float* o_weight_scale,
+    uint16_t* residual, const uint16_t* pre_ff_rms_weight, const uint8_t* up_weight, const uint8_t* gate_weight,
+    const uint8_t* down_weight, const float* up_weight_scale, const float* gate_weight_scale,
+    const float* down_weight_scale, const uint16_t* post_ff_rms_weight, const uint16_t* layer_scalar, int M,
+    void* stream) {
+    OParams o{x, post_attn_rms_weight, o_weight, o_weight_scale, ScaleKind::F32, residual};
+    FfnParams p{FfnFormat::FP8, residual, pre_ff_rms_weight, up_weight, gate_weight, down_weight,
+                up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
+    return o_ffn_common(o, p, M, stream);
+}
+
+int moa_sliding_attention_output_feedforward_mxfp4(
+    const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const float* o_weight_scale,
+    uint16_t* residual, const uint16_t* pre_ff_rms_weight, const uint8_t* up_weight_packed,
+    const uint8_t* gate_weight_packed, const uint8_t* down_weight_packed, const uint8_t* up_weight_scale,
+    const uint8_t* gate_weight_scale, const uint8_t* down_weight_scale, const uint16_t* post_ff_rms_weight,
+    const uint16_t* layer_scalar, int M, void* stream) {
+    OParams o{x, post_attn_rms_weight, o_weight, o_weight_scale, ScaleKind::F32, residual};
+    FfnParams p{FfnFormat::MXFP4, residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed,
+                down_weight_packed, up_weight_scale, gate_weight_scale, down_weight_scale, ScaleKind::F32,
+                nullptr, nullptr, nullptr, post_ff_rms_weight, layer_scalar};
+    return o_ffn_common(o, p, M, stream);
 }
 
 int moa_sliding_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* mask, uint16_t* out,

@@ -104,10 +104,9 @@ __device__ __forceinline__ void stall_hold(const Stall& st) {
     while (wall_clock64() - t0 < st.hold_ticks) __builtin_amdgcn_s_sleep(64);
 }
 
-// One wave of every workgroup b: publish its 16 outputs (bf16 bits dl[0..16)) and its partial sum
-// of squares (in row order).
-__device__ __forceinline__ void post_publish(PostSlots* slots, uint32_t tag, const uint32_t* dl, int lane) {
-    const int b = blockIdx.x;
+// One wave: publish workgroup b's 16 outputs (bf16 bits dl[0..16)) and their partial sum of
+// squares (in row order); post_publish for the calling workgroup.
+__device__ __forceinline__ void post_publish_at(PostSlots* slots, uint32_t tag, int b, const uint32_t* dl, int lane) {
     if (lane < kPostWgRows / 2) publish64(&slots->d[b][lane], tagged(tag, dl[2 * lane] | (dl[2 * lane + 1] << 16)));
     if (lane == 0) {
         float ss = 0.0f;
@@ -115,6 +114,10 @@ __device__ __forceinline__ void post_publish(PostSlots* slots, uint32_t tag, con
         for (int i = 0; i < kPostWgRows; ++i) ss = fmaf(bf2f(dl[i]), bf2f(dl[i]), ss);
         publish64(&slots->part[b], tagged(tag, __float_as_uint(ss)));
     }
+}
+
+__device__ __forceinline__ void post_publish(PostSlots* slots, uint32_t tag, const uint32_t* dl, int lane) {
+    post_publish_at(slots, tag, blockIdx.x, dl, lane);
 }
 
 // post_publish for workgroup b from registers (lane i < 16 holds output i): the same words and the
@@ -1414,63 +1417,43 @@ __device__ __forceinline__ void reload_stale(uint64_t (&w)[N], uint32_t tag, A a
 // 32 b), so that 240 readers of the same 61 KB do not request the same lines at the same time
 __device__ __forceinline__ int ffn_pword(int i) { return (threadIdx.x + kFfnBlock * i + blockIdx.x * 32) % (kL / 2); }
 
-template <FfnFormat F, ScaleKind SK, bool Hold = false>
-__global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uint32_t* tickets, uint32_t* err,
-                      Stall stall) {
+// Shared memory of the FFN half of the single-launch kernels (the kernel declares each array).
+struct FfnShared {
+    uint16_t* sh;  // [kL] normalised x (first kH), then the GeGLU row p
+    uint16_t* sx;  // [kH] normalised x, kept for a take-over of another block's rows
+    float* red;    // [kFfnWaves]
+    float* pl;     // [kFfnWaves * kUgRL]
+    uint32_t* dl;  // [kFfnWgRows] the workgroup's down outputs (bf16 bits)
+    uint32_t *s_tag, *s_expired, *s_stall;
+    int* s_victim;
+};
+
+// The FFN from the GeGLU values on, in a grid of kFfnGrid workgroups (ffn_fused_kernel and
+// o_ffn_fused_kernel): p through the tagged words, the down rows, then the post-norm hand-off or
+// (without a post-norm) each workgroup's own rows. pv: lane g < kUgRL of wave w holds GeGLU row
+// 8 g + w of the block (before its bf16 rounding); claim_old: what the block's claim exchange
+// returned (control wave, lane 0); dscale: down scale of row drow0 + lane (lanes < kFfnDownR);
+// control wave: r8 / w8 a leader's residual and post-norm weight values at post_leader_row (with
+// the post-norm), r1 the residual value of row 16 b + lane (without it), ls_bits the layer scalar.
+template <FfnFormat F, ScaleKind SK>
+__device__ __forceinline__ void ffn_down_post(const FfnParams& p, const FfnShared& s, float pv, uint32_t ep_tag,
+                                              uint32_t claim_old, uint16_t* res, int drow0, float dscale,
+                                              const uint4& r8, const uint4& w8, uint32_t r1, uint32_t ls_bits,
+                                              uint64_t* ptag, PostSlots* slots, uint32_t* err, const Stall& stall) {
     constexpr int KD = down_chunks<F>();
     constexpr int EPC = elems_per_chunk<F>();
-    __shared__ uint16_t sh[kL];  // normalised x (first kH), then the GeGLU row p
-    __shared__ uint16_t sx[kH];  // normalised x, kept for a take-over of another block's rows
-    __shared__ float red[kFfnWaves];
-    __shared__ float pl[kFfnWaves * kUgRL];
-    __shared__ uint32_t dl[kFfnWgRows];  // the workgroup's down outputs (bf16 bits)
-    __shared__ uint32_t s_tag, s_expired, s_stall;
-    __shared__ int s_victim;
-    if constexpr (Hold) stall_hold(stall);
     const int lane = lane_id(), wave = wave_id();
     const bool ctl = wave == kFfnCtl;
     const bool leader = blockIdx.x < kPostLeaders;
-    // The launch's tag: 15 counters of 16 workgroups each advance by one block per launch (every
-    // format shares them, so post-norm slot tags never repeat across formats). Needed only after
-    // up/gate.
-    uint32_t ep_tag = 0;
-    if (ctl && lane == 0)
-        ep_tag = epoch_tag<kFfnEpochPer>(epoch_add(tickets + (kTicketFfnEpoch + blockIdx.x % kFfnEpochCounters) * kTicketStride));
-    uint16_t* res = p.residual + (size_t)m0 * kH;
     const bool post = p.post_rms != nullptr;
-
-    const int drow0 = blockIdx.x * kFfnWgRows + wave * kFfnDownR;
-    const float dscale = row_scale<F, SK>(p.down_s, p.down_g, drow0 + min(lane, kFfnDownR - 1));
-
-    // Epilogue operands of the control wave, fetched now (off the critical path). With a post-norm
-    // a leader's lane l < 2 * kPostGroup owns 8 outputs of workgroup g + 8 (l / 2), rows
-    // (l % 2) * 8 ..; without one, every workgroup writes its own 16 outputs (lanes 0-15).
-    uint4 r8 = make_uint4(0, 0, 0, 0), w8 = make_uint4(0, 0, 0, 0);
-    uint32_t r1 = 0, ls_bits = 0;
-    if (ctl) {
-        if (p.layer_scalar) ls_bits = p.layer_scalar[0];
-        if (post && leader) {
-            r8 = ld16(res + post_leader_row(lane));
-            w8 = ld16(p.post_rms + post_leader_row(lane));
-        } else if (!post) {
-            r1 = res[blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1)];
-        }
-    }
-
-    // ---- up/gate: stage g reads L-rows base + 8g + wave; lane g's value is GeGLU row 8g + wave.
-    // Once the norm is done the block's claim goes out (its return arrives behind the first stage)
-    // and the normalised row is copied aside.
-    uint32_t claim_old = 0;
-    auto claim = [&] {
-        if (ctl && lane == 0)
-            claim_old = __hip_atomic_exchange(reinterpret_cast<uint32_t*>(&slots->claim[blockIdx.x]), ep_tag,
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x < kH / 8)
-            reinterpret_cast<uint4*>(sx)[threadIdx.x] = reinterpret_cast<const uint4*>(sh)[threadIdx.x];
-    };
-    const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
-    const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red, claim);
+    uint16_t* const sh = s.sh;
+    const uint16_t* const sx = s.sx;
+    float* const pl = s.pl;
+    uint32_t* const dl = s.dl;
+    uint32_t& s_tag = *s.s_tag;
+    uint32_t& s_expired = *s.s_expired;
+    uint32_t& s_stall = *s.s_stall;
+    int& s_victim = *s.s_victim;
     if (lane < kUgRL) pl[lane * kFfnWaves + wave] = pv;
     if (ctl && lane == 0) {
         s_tag = ep_tag;
@@ -1687,6 +1670,442 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
         post_publish_vals(slots, tag, b, v, lane);
     };
     post_leader<false>(slots, tag, res, r8, w8, p.layer_scalar != nullptr, lsv, lane, err, stall.steal_ticks, steal);
+}
+
+template <FfnFormat F, ScaleKind SK, bool Hold = false>
+__global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uint32_t* tickets, uint32_t* err,
+                      Stall stall) {
+    __shared__ uint16_t sh[kL];
+    __shared__ uint16_t sx[kH];
+    __shared__ float red[kFfnWaves];
+    __shared__ float pl[kFfnWaves * kUgRL];
+    __shared__ uint32_t dl[kFfnWgRows];
+    __shared__ uint32_t s_tag, s_expired, s_stall;
+    __shared__ int s_victim;
+    const FfnShared s{sh, sx, red, pl, dl, &s_tag, &s_expired, &s_stall, &s_victim};
+    if constexpr (Hold) stall_hold(stall);
+    const int lane = lane_id(), wave = wave_id();
+    const bool ctl = wave == kFfnCtl;
+    const bool leader = blockIdx.x < kPostLeaders;
+    // The launch's tag: 15 counters of 16 workgroups each advance by one block per launch (every
+    // format shares them, so post-norm slot tags never repeat across formats). Needed only after
+    // up/gate.
+    uint32_t ep_tag = 0;
+    if (ctl && lane == 0)
+        ep_tag = epoch_tag<kFfnEpochPer>(epoch_add(tickets + (kTicketFfnEpoch + blockIdx.x % kFfnEpochCounters) * kTicketStride));
+    uint16_t* res = p.residual + (size_t)m0 * kH;
+    const bool post = p.post_rms != nullptr;
+
+    const int drow0 = blockIdx.x * kFfnWgRows + wave * kFfnDownR;
+    const float dscale = row_scale<F, SK>(p.down_s, p.down_g, drow0 + min(lane, kFfnDownR - 1));
+
+    // Epilogue operands of the control wave, fetched now (off the critical path). With a post-norm
+    // a leader's lane l < 2 * kPostGroup owns 8 outputs of workgroup g + 8 (l / 2), rows
+    // (l % 2) * 8 ..; without one, every workgroup writes its own 16 outputs (lanes 0-15).
+    uint4 r8 = make_uint4(0, 0, 0, 0), w8 = make_uint4(0, 0, 0, 0);
+    uint32_t r1 = 0, ls_bits = 0;
+    if (ctl) {
+        if (p.layer_scalar) ls_bits = p.layer_scalar[0];
+        if (post && leader) {
+            r8 = ld16(res + post_leader_row(lane));
+            w8 = ld16(p.post_rms + post_leader_row(lane));
+        } else if (!post) {
+            r1 = res[blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1)];
+        }
+    }
+
+    // ---- up/gate: stage g reads L-rows base + 8g + wave; lane g's value is GeGLU row 8g + wave.
+    // Once the norm is done the block's claim goes out (its return arrives behind the first stage)
+    // and the normalised row is copied aside.
+    uint32_t claim_old = 0;
+    auto claim = [&] {
+        if (ctl && lane == 0)
+            claim_old = __hip_atomic_exchange(reinterpret_cast<uint32_t*>(&slots->claim[blockIdx.x]), ep_tag,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x < kH / 8)
+            reinterpret_cast<uint4*>(sx)[threadIdx.x] = reinterpret_cast<const uint4*>(sh)[threadIdx.x];
+    };
+    const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
+    const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red, claim);
+    ffn_down_post<F, SK>(p, s, pv, ep_tag, claim_old, res, drow0, dscale, r8, w8, r1, ls_bits, ptag, slots, err,
+                         stall);
+}
+
+// ============================================================= O -> FFN (one launch)
+// The tail of the reference's sliding-layer decode step (FO/src/host/runtime.rs:440-459, then
+// the mlp call at 543-571): ops::sliding_attention_output and then ops::decoder_feedforward on
+// the same residual row, in one grid of kFfnGrid workgroups of eight waves. The result has the
+// same bits as the two operators called one after the other.
+//
+// O phase: workgroup b computes O rows 16 b .. 16 b + 15 (two per wave, as o_fused_kernel) and
+// publishes them with their partial sum of squares through tagged post-norm words. Every
+// workgroup -- not only leaders -- then reads all 240 workgroups' words and applies O's post-norm
+// and residual add itself, summing the partial sums in the leaders' order (post_leader), so
+// every workgroup holds the same bits. The residual row after O (r1) never goes to memory: it is
+// the FFN's input row, and stays in LDS for the FFN's own residual add.
+//
+// The FFN's first two up/gate ring stages go out during the O phase: the first behind O's weight
+// loads, the second behind the reads of O's words. A CU returns its loads in order, so those
+// reads land once the first stage has (about 2 us after O's weights), when normally every
+// workgroup has published; the second stage is in flight behind them, so the weight stream does
+// not pause for O's grid-wide dependency.
+//
+// Tags: the FFN's epoch counters give the launch one tag for its three hand-offs; O's words live
+// in a slot area only this kernel writes (the FFN's p and post-norm words are shared with
+// ffn_fused_kernel, whose tags come from the same counters).
+//
+// Take-over: a workgroup that has waited stall.steal_ticks for O's words computes the lowest
+// missing workgroup's O rows itself (they depend only on the attention row and W_o) and
+// publishes them; several workgroups may do so for one, with the same bits. From the GeGLU
+// values on, the FFN's take-overs apply (ffn_down_post). A workgroup that started so late that
+// the leaders had already written residual rows computes a wrong r1, but its up/gate block has
+// then been claimed by another workgroup, so it publishes no GeGLU value; its O and down rows
+// depend only on the attention row, p and the weights, and a leader's own residual rows are
+// written by it alone.
+// O's post-norm words of the single-launch O -> FFN kernel, in kOfnReplicas copies: every
+// workgroup reads all 240 workgroups' words, and 240 coherent reads of each line serialise where
+// the line lives; workgroup b reads copy b % kOfnReplicas.
+constexpr int kOfnReplicas = kOfnCopies;
+
+// One wave: publish workgroup b's outputs (dl) and partial sum in every copy -- lane l writes word
+// l % 9 of copy l / 9 (seven copies per store instruction).
+__device__ __forceinline__ void ofn_publish(PostSlots* copies, uint32_t tag, int b, const uint32_t* dl, int lane) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPostWgRows; ++i) ss = fmaf(bf2f(dl[i]), bf2f(dl[i]), ss);  // post_publish's order
+    const int w = lane % 9;
+    const uint64_t v = w < 8 ? tagged(tag, dl[2 * w] | (dl[2 * w + 1] << 16)) : tagged(tag, __float_as_uint(ss));
+#pragma unroll
+    for (int c0 = 0; c0 < kOfnReplicas; c0 += 7) {
+        const int c = c0 + lane / 9;
+        if (lane < 63 && c < kOfnReplicas) publish64(w < 8 ? &copies[c].d[b][w] : &copies[c].part[b], v);
+    }
+}
+
+template <FfnFormat F, ScaleKind SKO, ScaleKind SK, bool Hold = false>
+__global__ __launch_bounds__(kFfnBlock) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void o_ffn_fused_kernel(OParams o, FfnParams p, int m0, PostSlots* oslots, uint64_t* ptag, PostSlots* slots,
+                        uint32_t* tickets, uint32_t* err, Stall stall) {
+    constexpr int EPC = elems_per_chunk<F>();
+    constexpr int RB = row_bytes<F>(kH);
+    constexpr int SB = scale_row_bytes<F>(kH);
+    constexpr int KI = (RB + 1023) / 1024;
+    constexpr int KO = kQs / 1024;  // O weight chunks per row and lane
+    constexpr int RL = kUgRL;
+    static_assert(kFfnWaves * kORowsW == kPostWgRows && kFfnGrid == kPostGrid, "O rows per workgroup");
+    static_assert(kQs == 8 * kFfnBlock, "one 16-byte chunk of the attention row per thread");
+    static_assert(kH == 16 * kPostGrid, "thread t < 240 owns O workgroup t's 16 outputs");
+    __shared__ uint16_t sh[kL];
+    __shared__ uint16_t sx[kH];
+    __shared__ float red[kFfnWaves];
+    __shared__ float pl[kFfnWaves * kUgRL];
+    __shared__ uint32_t dl[kFfnWgRows];
+    __shared__ uint32_t s_tag, s_expired, s_stall;
+    __shared__ int s_victim;
+    __shared__ uint16_t xs[kQs];        // the attention row
+    __shared__ uint16_t r1s[kH];        // the residual row after O
+    __shared__ uint32_t odl[kPostWgRows];  // this workgroup's O outputs (bf16 bits)
+    __shared__ uint32_t vdl[kPostWgRows];  // a taken-over workgroup's
+    __shared__ int s_ovictim;
+    const FfnShared s{sh, sx, red, pl, dl, &s_tag, &s_expired, &s_stall, &s_victim};
+    if constexpr (Hold) stall_hold(stall);
+    const int lane = lane_id(), wave = wave_id(), t = threadIdx.x;
+    const bool ctl = wave == kFfnCtl;
+    const bool leader = blockIdx.x < kPostLeaders;
+    const bool post = p.post_rms != nullptr;
+    const bool own = t < kPostGrid;  // owns O workgroup t's outputs: rows 16 t .. 16 t + 15
+    uint16_t* res = p.residual + (size_t)m0 * kH;
+    // The launch's tag, before any load (as ffn_fused_kernel): the control wave waits for the
+    // exchange's return where the result is first held, and issued behind the O weights that wait
+    // would cover them too, delaying its share of up/gate stage 0.
+    uint32_t ep_tag = 0;
+    if (ctl && lane == 0)
+        ep_tag = epoch_tag<kFfnEpochPer>(epoch_add(tickets + (kTicketFfnEpoch + blockIdx.x % kFfnEpochCounters) * kTicketStride));
+
+    // Operands first in every wave's load order: the attention row (a 16-byte chunk per thread);
+    // thread t < 240 its 16 residual values and both norm weights there; the scales; the control
+    // wave its epilogue operands.
+    const uint4 xq = ld16(o.x + (size_t)m0 * kQs + t * 8);
+    uint4 rv0 = make_uint4(0, 0, 0, 0), rv1 = rv0, wo0 = rv0, wo1 = rv0;
+    RmsStage st{};
+    if (own) {
+        rv0 = ld16(res + t * 16);
+        rv1 = ld16(res + t * 16 + 8);
+        wo0 = ld16(o.post_rms + t * 16);
+        wo1 = ld16(o.post_rms + t * 16 + 8);
+        st.w0 = ld16(p.pre_rms + t * 16);
+        st.w1 = ld16(p.pre_rms + t * 16 + 8);
+    }
+    const int orow0 = blockIdx.x * kPostWgRows + wave * kORowsW;
+    const float oscale = load_scale<SKO>(o.os, orow0 + min(lane, kORowsW - 1));
+    const int lbase = blockIdx.x * (kFfnWaves * RL) + wave;
+    const int lrow = lbase + min(lane, RL - 1) * kFfnWaves;
+    const float su = row_scale<F, SK>(p.up_s, p.up_g, lrow);
+    const float sg = row_scale<F, SK>(p.gate_s, p.gate_g, lrow);
+    const int drow0 = blockIdx.x * kFfnWgRows + wave * kFfnDownR;
+    const float dscale = row_scale<F, SK>(p.down_s, p.down_g, drow0 + min(lane, kFfnDownR - 1));
+    uint4 w8 = make_uint4(0, 0, 0, 0);
+    uint32_t ls_bits = 0;
+    if (ctl) {
+        if (p.layer_scalar) ls_bits = p.layer_scalar[0];
+        if (post && leader) w8 = ld16(p.post_rms + post_leader_row(lane));
+    }
+    __syncthreads();  // every wave's operand loads are issued ahead of the weight loads below
+
+    // O's two rows per wave, then up/gate stage 0
+    uint4 wq[kORowsW][KO];
+#pragma unroll
+    for (int r = 0; r < kORowsW; ++r)
+#pragma unroll
+        for (int j = 0; j < KO; ++j) wq[r][j] = ld_stream(o.ow + (size_t)(orow0 + r) * kQs + j * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    Chunk<F> ring[2][2][KI];
+    auto issue = [&](int g, Chunk<F> (&dst)[2][KI]) {
+        const int l = lbase + g * kFfnWaves;
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            const bool valid = j * 1024 + lane * 16 < RB;
+            load_chunk<F>(dst[0][j], p.up + (size_t)l * RB, (const uint8_t*)p.up_s + (size_t)l * SB, j, lane, valid);
+            load_chunk<F>(dst[1][j], p.gate + (size_t)l * RB, (const uint8_t*)p.gate_s + (size_t)l * SB, j, lane, valid);
+        }
+    };
+    *reinterpret_cast<uint4*>(xs + t * 8) = xq;
+    __syncthreads();
+
+    // this wave's two rows of an O workgroup: bf16((x . W_o[row]) * scale) into dst
+    // (generate_references.py:265-274)
+    auto o_rows = [&](const uint4 (&w)[kORowsW][KO], float sc, uint32_t* dst) {
+        float acc[kORowsW];
+#pragma unroll
+        for (int r = 0; r < kORowsW; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KO; ++j) {
+            uint32_t x[8];
+            lds_pairs<16>(xs, j * 1024 + lane * 16, x);
+#pragma unroll
+            for (int r = 0; r < kORowsW; ++r) acc[r] = dot_fp8x16_bf16(x, w[r][j], acc[r]);
+        }
+        float mine = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kORowsW; ++r) {
+            const float d = wave_sum(acc[r]);
+            if (lane == r) mine = d;
+        }
+        if (lane < kORowsW) dst[wave * kORowsW + lane] = f2bf(mine * sc);
+    };
+    o_rows(wq, oscale, odl);
+    if (ctl && lane == 0) {
+        s_tag = ep_tag;
+        s_expired = 0u;
+        s_stall = 0u;
+    }
+    __syncthreads();  // odl complete; the tag in LDS
+    const uint32_t tag = s_tag;
+    if (ctl) ofn_publish(oslots, tag, blockIdx.x, odl, lane);
+    // The publish leaves the CU ahead of every later load of the workgroup: a store queued behind
+    // stage 0 would reach memory only once stage 0 has landed, and the other workgroups' reads
+    // would find it missing.
+    __syncthreads();
+
+    // O's words. A CU returns its loads in the order they were issued, but a load reads memory
+    // when it is issued: a read queued behind a prefetch comes back late AND holds what memory
+    // held at its issue. So the words are read twice at most, each read ahead of one up/gate
+    // stage: the first right after this workgroup's publish (nothing but landed O weights ahead
+    // of it: it comes back within a round trip, current for every workgroup that published by
+    // then), stage 0 behind it; the second goes out once the first is back -- by then normally
+    // every workgroup has published -- with stage 1 behind it, and lands with stage 0, which the
+    // up/gate loop needs next anyway. The 2160 words are read flat and coalesced (word j =
+    // t + 512 k: d[0][0] .. d[239][7], then part[0 .. 239]) and regrouped through LDS. The
+    // workgroup's own words count as current -- its reads could overtake its own stores -- and
+    // are taken from odl. Reads and checks are branch-free straight-line code, so each check waits
+    // for its own read alone (a branch around the reads, or a check at the head of a loop, makes
+    // the compiler wait for every load in flight).
+    constexpr int kOWords = 9 * kPostGrid;
+    constexpr int kOR = (kOWords + kFfnBlock - 1) / kFfnBlock;  // reads per thread
+    PostSlots* const mine = oslots + blockIdx.x % kOfnReplicas;
+    auto jof = [&](int k) { return min(t + kFfnBlock * k, kOWords - 1); };
+    auto wg_of = [&](int k) { const int j = jof(k); return j < 8 * kPostGrid ? j >> 3 : j - 8 * kPostGrid; };
+    auto waddr = [&](int k) {
+        const int j = jof(k);
+        return j < 8 * kPostGrid ? &mine->d[0][0] + j : &mine->part[j - 8 * kPostGrid];
+    };
+    uint64_t ow[kOR];
+    auto current = [&] {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) ok = ok && ((uint32_t)(ow[k] >> 32) == tag || wg_of(k) == (int)blockIdx.x);
+        return ok;
+    };
+#pragma unroll
+    for (int k = 0; k < kOR; ++k) ow[k] = collect64(waddr(k));
+    // every wave's read goes out before any wave's stage: a read queued behind another wave's
+    // stage would come back with that stage
+    __syncthreads();
+    issue(0, ring[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        // the second read once the first is back (the tag compares come first: the barrier
+        // waits for every wave's), the words the first read found current kept
+        bool keep[kOR];
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) keep[k] = (uint32_t)(ow[k] >> 32) == tag;
+        __syncthreads();
+        uint64_t again[kOR];
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) again[k] = collect64(waddr(k));
+        __syncthreads();
+        issue(1, ring[1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) ow[k] = keep[k] ? ow[k] : again[k];
+    }
+    if (!__syncthreads_and(current())) {
+        // Rare (a workgroup started late): poll until every word is current, taking a missing
+        // workgroup's O rows over after stall.steal_ticks.
+        const uint64_t t0 = wall_clock64();
+        uint64_t tsteal = t0;
+        for (;;) {
+            const uint64_t now = wall_clock64();
+            if (__syncthreads_or(now - t0 > kSpinTicks)) {
+                // nothing of this launch is stored or published by this workgroup; the others'
+                // waits for its GeGLU values take them over
+                if (t == 0) atomicOr(err, kErrSpinTimeout);
+                return;
+            }
+            if (__builtin_expect(__syncthreads_or(now - tsteal > stall.steal_ticks), 0)) {
+                // the lowest workgroup with a stale word: its rows, two per wave, as its own waves
+                // compute them
+                if (t == 0) s_ovictim = kPostGrid;
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < kOR; ++k)
+                    if ((uint32_t)(ow[k] >> 32) != tag && wg_of(k) != (int)blockIdx.x) atomicMin(&s_ovictim, wg_of(k));
+                __syncthreads();
+                const int v = s_ovictim;
+                const int vrow0 = v * kPostWgRows + wave * kORowsW;
+                uint4 vq[kORowsW][KO];
+#pragma unroll
+                for (int r = 0; r < kORowsW; ++r)
+#pragma unroll
+                    for (int j = 0; j < KO; ++j)
+                        vq[r][j] = ld_stream(o.ow + (size_t)(vrow0 + r) * kQs + j * 1024 + lane * 16);
+                o_rows(vq, load_scale<SKO>(o.os, vrow0 + min(lane, kORowsW - 1)), vdl);
+                __syncthreads();
+                if (ctl) ofn_publish(oslots, tag, v, vdl, lane);
+                if (t == 0) atomicAdd(err + kErrTakeOvers, 1u);
+                tsteal = wall_clock64();
+            } else {
+                __builtin_amdgcn_s_sleep(1);
+            }
+            reload_stale(ow, tag, waddr, std::make_integer_sequence<int, kOR>{});
+            if (__syncthreads_and(current())) break;
+        }
+        // Every load of this path complete: after the loop the compiler cannot count the loads in
+        // flight, and without this wait it would make the common path below wait for all of them
+        // (stage 1 included) wherever it first uses a register loaded before the loop.
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+
+    // The words into LDS (the FFN's p row area: free until the pre-norm writes it), this
+    // workgroup's own from odl; then O's post-norm and residual (FO/src/device/shared/
+    // rmsnorm.rs:204-296, projection.rs:577-605): r1 = bf16(r + bf16(bf16(d * inv) * w_post)),
+    // inv from the 240 partial sums in post_leader's order (lane l: parts l, l + 64, l + 128,
+    // l + 192; then the wave butterfly), in every wave.
+    uint64_t* const owl = reinterpret_cast<uint64_t*>(sh);
+    static_assert(sizeof(uint64_t) * kOWords <= sizeof(uint16_t) * kL, "O's words fit the p row area");
+    {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kPostWgRows; ++i) ss = fmaf(bf2f(odl[i]), bf2f(odl[i]), ss);  // post_publish's order
+#pragma unroll
+        for (int k = 0; k < kOR; ++k) {
+            const int j = t + kFfnBlock * k;
+            const int i = j & 7;
+            const uint64_t own_word = j < 8 * kPostGrid ? tagged(tag, odl[2 * i] | (odl[2 * i + 1] << 16))
+                                                         : tagged(tag, __float_as_uint(ss));
+            if (j < kOWords) owl[j] = wg_of(k) == (int)blockIdx.x ? own_word : ow[k];
+        }
+    }
+    __syncthreads();
+    {
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < (kPostGrid + 63) / 64; ++i) {
+            const int b = lane + 64 * i;
+            tot += b < kPostGrid ? __uint_as_float((uint32_t)owl[8 * kPostGrid + b]) : 0.0f;
+        }
+        const float oinv = rms_inverse(wave_sum(tot), kH);
+        if (own) {
+            const uint32_t rw[8] = {rv0.x, rv0.y, rv0.z, rv0.w, rv1.x, rv1.y, rv1.z, rv1.w};
+            const uint32_t ww[8] = {wo0.x, wo0.y, wo0.z, wo0.w, wo1.x, wo1.y, wo1.z, wo1.w};
+            uint32_t o8[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t dq = (uint32_t)owl[8 * t + k];
+                uint32_t pair = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float d = bf2f((dq >> (16 * h)) & 0xffffu);
+                    const float n = rbf((d * oinv) * bf2f((ww[k] >> (16 * h)) & 0xffffu));
+                    pair |= f2bf(bf2f((rw[k] >> (16 * h)) & 0xffffu) + n) << (16 * h);
+                }
+                o8[k] = pair;
+            }
+            st.x0 = make_uint4(o8[0], o8[1], o8[2], o8[3]);
+            st.x1 = make_uint4(o8[4], o8[5], o8[6], o8[7]);
+            *reinterpret_cast<uint4*>(r1s + t * 16) = st.x0;
+            *reinterpret_cast<uint4*>(r1s + t * 16 + 8) = st.x1;
+        }
+    }
+    // the FFN's pre-norm of r1 (as ffn_fused_kernel's of the residual row), the block's claim and
+    // the copy of the normalised row kept for take-overs
+    rms_finish_bf16<kFfnWaves>(st, sh, red);
+    uint32_t claim_old = 0;
+    if (ctl && lane == 0)
+        claim_old = __hip_atomic_exchange(reinterpret_cast<uint32_t*>(&slots->claim[blockIdx.x]), tag,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t < kH / 8) reinterpret_cast<uint4*>(sx)[t] = reinterpret_cast<const uint4*>(sh)[t];
+
+    // up/gate (as up_gate_rows): stage g reads L-rows lbase + 8 g; stages g + 2 go out once stage
+    // g's registers are consumed
+    uint32_t xv[KI][EPC / 2];
+#pragma unroll
+    for (int j = 0; j < KI; ++j) {
+        const int e0 = j * 64 * EPC + lane * EPC;
+        if (e0 < kH) lds_pairs<EPC>(sh, e0, xv[j]);
+        else {
+#pragma unroll
+            for (int i = 0; i < EPC / 2; ++i) xv[j][i] = 0u;
+        }
+    }
+    float pv = 0.0f;
+#pragma unroll
+    for (int g = 0; g < RL; ++g) {
+        Chunk<F> (&src)[2][KI] = ring[g % 2];
+        float du = 0.0f, dg = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KI; ++j) {
+            du = chunk_dot2<F>(xv[j], src[0][j], du);
+            dg = chunk_dot2<F>(xv[j], src[1][j], dg);
+        }
+        if (g + 2 < RL) issue(g + 2, ring[g % 2]);
+        du = wave_sum(du);
+        dg = wave_sum(dg);
+        const float up = proj_commit<F>(du, __shfl(su, g, kWave));
+        const float gate = proj_commit<F>(dg, __shfl(sg, g, kWave));
+        if (lane == g) pv = rbf(gelu_tanh(gate)) * up;  // gemma4.py:197
+    }
+
+    // the FFN's residual values from r1: a leader's rows with the post-norm, the workgroup's own
+    // rows without it
+    uint4 r8 = make_uint4(0, 0, 0, 0);
+    uint32_t r1 = 0;
+    if (ctl) {
+        if (post && leader) r8 = *reinterpret_cast<const uint4*>(r1s + post_leader_row(lane));
+        else if (!post) r1 = r1s[blockIdx.x * kFfnWgRows + min(lane, kFfnWgRows - 1)];
+    }
+    ffn_down_post<F, SK>(p, s, pv, tag, claim_old, res, drow0, dscale, r8, w8, r1, ls_bits, ptag, slots, err, stall);
 }
 
 // ========================================================== raw projection
@@ -1933,6 +2352,29 @@ hipError_t launch_ffn_decode(const FfnParams& p, int M, hipStream_t s, DevCtx* c
         case FfnFormat::MXFP4: return ffn_decode_impl<FfnFormat::MXFP4, ScaleKind::F32>(p, M, s, ctx);
     }
     return hipErrorInvalidValue;
+}
+
+template <FfnFormat F, ScaleKind SKO, ScaleKind SK>
+static bool o_ffn_fused(const OParams& o, const FfnParams& p, hipStream_t s, DevCtx* ctx, hipError_t* e) {
+    if (!fits_resident(ctx->o_ffn_fused[(int)F], o_ffn_fused_kernel<F, SKO, SK>, kFfnBlock, kFfnGrid, ctx)) return false;
+    *e = launch_fused(o_ffn_fused_kernel<F, SKO, SK>, o_ffn_fused_kernel<F, SKO, SK, true>, dim3(kFfnGrid), kFfnBlock, s,
+                      o, p, 0, reinterpret_cast<PostSlots*>(ctx->ofn_part), ctx->ffn_ptag,
+                      reinterpret_cast<PostSlots*>(ctx->ffn_part), ctx->tickets, ctx->err);
+    return true;
+}
+
+bool launch_o_ffn_fused(const OParams& o, const FfnParams& p, hipStream_t s, DevCtx* ctx, hipError_t* e) {
+    const bool of32 = o.scale_kind == ScaleKind::F32;
+    switch (p.fmt) {
+        case FfnFormat::FP8:
+            return of32 && p.scale_kind == ScaleKind::F32 &&
+                   o_ffn_fused<FfnFormat::FP8, ScaleKind::F32, ScaleKind::F32>(o, p, s, ctx, e);
+        case FfnFormat::NVFP4:
+            return !of32 && o_ffn_fused<FfnFormat::NVFP4, ScaleKind::BF16, ScaleKind::F32>(o, p, s, ctx, e);
+        case FfnFormat::MXFP4:
+            return of32 && o_ffn_fused<FfnFormat::MXFP4, ScaleKind::F32, ScaleKind::F32>(o, p, s, ctx, e);
+    }
+    return false;
 }
 
 hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s) {

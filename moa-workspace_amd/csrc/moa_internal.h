@@ -54,6 +54,7 @@ constexpr size_t kFattnPartFloats = (size_t)kFattnRecords * kFaRec;
 constexpr int kFfnPartSlots = 256;
 constexpr int kFfnSlotWords = kFfnPartSlots * 10;
 constexpr int kQkvSlotWords = 32 * 8;
+constexpr int kOfnCopies = 8;  // copies of O's post-norm words in the single-launch O -> FFN kernel
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
@@ -73,6 +74,7 @@ struct DevCtx {
     uint64_t* ffn_part = nullptr;  // tagged hand-off words of the single-launch FFN (kFfnSlotWords)
     uint64_t* ffn_ptag = nullptr;  // [kL / 2] tagged GeGLU pairs of the single-launch FP8 FFN (only it writes them)
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
+    uint64_t* ofn_part = nullptr; // O's post-norm words of the single-launch O -> FFN (kOfnCopies x kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
     float* attn_part = nullptr;   // sliding_attention split partials (kAttnPartFloats)
     float* fattn_part = nullptr;  // full-attention page partials (kFattnPartFloats)
@@ -82,6 +84,7 @@ struct DevCtx {
     int8_t o_fused[2] = {-1, -1};                    // per scale kind
     int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
     int8_t full_o_fused[2] = {-1, -1};               // the same for full_attention_output
+    int8_t o_ffn_fused[3] = {-1, -1, -1};            // the single-launch O -> FFN, per FFN format
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
@@ -139,6 +142,11 @@ hipError_t launch_qkv_decode(const QkvParams& p, int M, hipStream_t s, DevCtx* c
 hipError_t launch_o_decode(const OParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_decode(const FfnParams& p, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_proj_decode(const ProjParams& p, int M, hipStream_t s);
+// One token row of sliding_attention_output followed by decoder_feedforward on the same residual
+// (o.residual == p.residual), in one launch. Returns false, launching nothing, when that grid cannot
+// be resident at once or no single-launch kernel covers the operand types (FP8 FFN with f32 O
+// scales, NVFP4 with bf16 O scales, MXFP4 with f32 O scales); *e is the launch's status otherwise.
+bool launch_o_ffn_fused(const OParams& o, const FfnParams& p, hipStream_t s, DevCtx* ctx, hipError_t* e);
 
 // Full-attention layers: ops::full_project_qkv (QkvParams with vw / vs unused; k_cache / v_cache
 // are the position's page) and ops::full_attention_output (OParams with div set).

@@ -71,6 +71,9 @@ SIGNATURES = {
     "moa_decoder_feedforward_fp8": [P] * 10 + [I32, P],
     "moa_decoder_feedforward_mxfp4": [P] * 10 + [I32, P],
     "moa_decoder_feedforward_fp8_noalloc": [P] * 10 + [I32, P],
+    "moa_sliding_attention_output_feedforward": [P] * 17 + [I32, P],
+    "moa_sliding_attention_output_feedforward_fp8": [P] * 14 + [I32, P],
+    "moa_sliding_attention_output_feedforward_mxfp4": [P] * 14 + [I32, P],
     "moa_fp8_scaled_projection": [P] * 4 + [I32, I32, I32, P],
     "moa_format_selftest": [P, P],
     "moa_test_epoch_layout": [I32, C.POINTER(C.c_int), C.POINTER(C.c_int)],

@@ -249,6 +249,76 @@ def decoder_feedforward_mxfp4(residual, pre_ff_rms_weight, up_weight_packed, gat
     _lib.call("moa_decoder_feedforward_mxfp4", *args, M, _stream(residual))
 
 
+def _o_args(x, post_attn_rms_weight, o_weight, o_weight_scale, residual, scale_dtypes):
+    M = _rows(x, QS, "x")
+    return M, [
+        _ptr(x, "x", _BF16), _ptr(post_attn_rms_weight, "post_attn_rms_weight", _BF16, H),
+        _ptr(o_weight, "o_weight", _U8, H * QS), _ptr(o_weight_scale, "o_weight_scale", scale_dtypes, H),
+        _ptr(residual, "residual", _BF16, M * H),
+    ]
+
+
+def sliding_attention_output_feedforward(x, post_attn_rms_weight, o_weight, o_weight_scale, residual,
+                                         pre_ff_rms_weight, up_weight_packed, gate_weight_packed, down_weight_packed,
+                                         up_weight_scale, gate_weight_scale, down_weight_scale, up_global_scale,
+                                         gate_global_scale, down_global_scale, post_ff_rms_weight,
+                                         layer_scalar) -> None:
+    """The tail of the reference's sliding-layer step (FO/src/host/runtime.rs:440-459, 543-571):
+    sliding_attention_output (bf16 O scales, as ops.rs:136) then decoder_feedforward (NVFP4) on the
+    same residual, in place. One launch per token row; the same bits as the two calls in turn."""
+    M, args = _o_args(x, post_attn_rms_weight, o_weight, o_weight_scale, residual, _BF16)
+    args += [
+        _ptr(pre_ff_rms_weight, "pre_ff_rms_weight", _BF16, H),
+        _ptr(up_weight_packed, "up_weight_packed", _U8, L * H // 2),
+        _ptr(gate_weight_packed, "gate_weight_packed", _U8, L * H // 2),
+        _ptr(down_weight_packed, "down_weight_packed", _U8, H * L // 2),
+        _ptr(up_weight_scale, "up_weight_scale", _U8, L * H // 16),
+        _ptr(gate_weight_scale, "gate_weight_scale", _U8, L * H // 16),
+        _ptr(down_weight_scale, "down_weight_scale", _U8, H * L // 16),
+        _ptr(up_global_scale, "up_global_scale", _F32, 1), _ptr(gate_global_scale, "gate_global_scale", _F32, 1),
+        _ptr(down_global_scale, "down_global_scale", _F32, 1),
+        _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
+    ]
+    _lib.call("moa_sliding_attention_output_feedforward", *args, M, _stream(x))
+
+
+def sliding_attention_output_feedforward_fp8(x, post_attn_rms_weight, o_weight, o_weight_scale, residual,
+                                             pre_ff_rms_weight, up_weight, gate_weight, down_weight, up_weight_scale,
+                                             gate_weight_scale, down_weight_scale, post_ff_rms_weight=None,
+                                             layer_scalar=None) -> None:
+    """sliding_attention_output (f32 O scales) then decoder_feedforward_fp8 on the same residual
+    (BASELINE configs 1 then 0), in place: one launch per token row, the same bits as the two calls."""
+    M, args = _o_args(x, post_attn_rms_weight, o_weight, o_weight_scale, residual, _F32)
+    args += [
+        _ptr(pre_ff_rms_weight, "pre_ff_rms_weight", _BF16, H),
+        _ptr(up_weight, "up_weight", _U8, L * H), _ptr(gate_weight, "gate_weight", _U8, L * H),
+        _ptr(down_weight, "down_weight", _U8, H * L), _ptr(up_weight_scale, "up_weight_scale", _F32, L),
+        _ptr(gate_weight_scale, "gate_weight_scale", _F32, L), _ptr(down_weight_scale, "down_weight_scale", _F32, H),
+        _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
+    ]
+    _lib.call("moa_sliding_attention_output_feedforward_fp8", *args, M, _stream(x))
+
+
+def sliding_attention_output_feedforward_mxfp4(x, post_attn_rms_weight, o_weight, o_weight_scale, residual,
+                                               pre_ff_rms_weight, up_weight_packed, gate_weight_packed,
+                                               down_weight_packed, up_weight_scale, gate_weight_scale,
+                                               down_weight_scale, post_ff_rms_weight=None,
+                                               layer_scalar=None) -> None:
+    """sliding_attention_output (f32 O scales) then decoder_feedforward_mxfp4 on the same residual."""
+    M, args = _o_args(x, post_attn_rms_weight, o_weight, o_weight_scale, residual, _F32)
+    args += [
+        _ptr(pre_ff_rms_weight, "pre_ff_rms_weight", _BF16, H),
+        _ptr(up_weight_packed, "up_weight_packed", _U8, L * H // 2),
+        _ptr(gate_weight_packed, "gate_weight_packed", _U8, L * H // 2),
+        _ptr(down_weight_packed, "down_weight_packed", _U8, H * L // 2),
+        _ptr(up_weight_scale, "up_weight_scale", _U8, L * H // 32),
+        _ptr(gate_weight_scale, "gate_weight_scale", _U8, L * H // 32),
+        _ptr(down_weight_scale, "down_weight_scale", _U8, H * L // 32),
+        _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
+    ]
+    _lib.call("moa_sliding_attention_output_feedforward_mxfp4", *args, M, _stream(x))
+
+
 def fp8_scaled_projection(x, w, scale, out) -> None:
     """scaled_projection (FO/scripts/generate_references.py:265-274): out = bf16((x . W^T) * scale)."""
     N, K = w.shape

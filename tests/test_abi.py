@@ -51,6 +51,9 @@ def _null(n):
     ("moa_full_attention_first_page", 7, (1, None)),
     ("moa_full_attention_page", 7, (1, None)),
     ("moa_full_attention_output", 6, (1, None)),
+    ("moa_sliding_attention_output_feedforward", 17, (1, None)),
+    ("moa_sliding_attention_output_feedforward_fp8", 14, (1, None)),
+    ("moa_sliding_attention_output_feedforward_mxfp4", 14, (1, None)),
 ])
 def test_null_pointers_rejected_on_host(fn, nptr, tail):
     lib = _lib.load()

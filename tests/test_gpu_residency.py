@@ -17,6 +17,7 @@ from moa_amd import _lib, synth
 from test_gpu_ffn import gpu_fp8, gpu_mxfp4, gpu_nvfp4
 from test_gpu_full import out_gpu as full_o_gpu
 from test_gpu_o import run_gpu as o_gpu
+from test_gpu_o_ffn import gpu_fused as o_ffn_gpu
 from test_gpu_qkv import run_gpu as qkv_gpu
 
 pytestmark = pytest.mark.gpu
@@ -56,7 +57,7 @@ def calls():
     """One closure per single-launch kernel (and FFN mode): fixed inputs, host bits out."""
     need_gpu()
     f, m, n = synth.cfg_ffn_fp8(5), synth.cfg_ffn_mxfp4(5), synth.ref_ffn_inputs(1)
-    o, fo, q = synth.cfg_o(5), synth.cfg_full_o(5), synth.cfg_qkv(5)
+    o, fo, q, ro = synth.cfg_o(5), synth.cfg_full_o(5), synth.cfg_qkv(5), synth.ref_o_inputs(1)
     return {
         "ffn_fp8": lambda: gpu_fp8(f),
         "ffn_fp8_no_post_norm": lambda: gpu_fp8(f, post=False, ls=False),
@@ -64,6 +65,8 @@ def calls():
         "ffn_mxfp4": lambda: gpu_mxfp4(m),
         "ffn_nvfp4": lambda: gpu_nvfp4(n),
         "o": lambda: o_gpu(o),
+        "o_ffn_fp8": lambda: o_ffn_gpu("fp8", o, f),
+        "o_ffn_nvfp4": lambda: o_ffn_gpu("nvfp4", ro, n),
         "full_o": lambda: full_o_gpu(fo),
         "qkv": lambda: np.concatenate([a.reshape(-1) for a in qkv_gpu(q)]),
     }
