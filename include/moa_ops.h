@@ -41,7 +41,8 @@ extern "C" {
 #define MOA_ERROR_MISALIGNED (-2)    /* pointer not 16-byte aligned */
 #define MOA_ERROR_HIP (-3)           /* a HIP runtime call failed */
 #define MOA_ERROR_NO_DEVICE (-4)     /* no usable gfx950 device */
-#define MOA_ERROR_DEVICE_STATE (-5)  /* a kernel flagged a bad device-resident argument */
+#define MOA_ERROR_DEVICE_STATE (-5)  /* a kernel flagged a bad device-resident argument, or the
+                                        device's state is tripped (see moa_clear_device_state) */
 
 #define MOA_DEVERR_ROPE_OFFSET 1u /* rope_offset not a multiple of 512 or past the table */
 #define MOA_DEVERR_KV_OFFSET 2u   /* kv_offset not a multiple of 4096 or past the ring */
@@ -50,7 +51,10 @@ extern "C" {
                                       expired store nothing: with the post-norm, the residual rows
                                       behind an expired leader keep their input values, but rows of
                                       other leaders may hold the result, so restore the outputs
-                                      from a copy before calling again. */
+                                      from a copy before calling again. Once moa_device_errors has
+                                      returned this bit, the device's state is tripped: every call
+                                      that computes on it, and moa_init, return
+                                      MOA_ERROR_DEVICE_STATE until moa_clear_device_state. */
 
 /* Library version string. */
 const char* moa_version(void);
@@ -66,8 +70,15 @@ int moa_init(int device);
 
 /* Synchronises `stream`, returns the OR of device-side error bits raised since the last call
  * (MOA_DEVERR_*) in *bits, and clears them. Reads the error word of each scratch that exists on
- * the current device and creates none, so it allocates nothing. */
+ * the current device and creates none, so it allocates nothing. MOA_DEVERR_SPIN_TIMEOUT among
+ * the bits trips the device's state (see below). */
 int moa_device_errors(void* stream, uint32_t* bits);
+
+/* No counterpart in the reference, whose operators cannot fail (FO/src/bin/test_kernels.rs:536
+ * unwraps). Acknowledges a tripped state of `device` -- a one-token call's wait expired and the
+ * caller has restored that call's outputs -- so that calls compute again. Returns MOA_SUCCESS
+ * whether or not the state was tripped. */
+int moa_clear_device_state(int device);
 
 /* ops::sliding_project_qkv -- FO/src/ops.rs:37-76.
  * x bf16 [M,3840]; q_weight E4M3 [4096,3840]; k_weight, v_weight E4M3 [2048,3840] (row =
@@ -297,6 +308,10 @@ int moa_test_take_overs(uint32_t* count);
  * hipMalloc'd scratch of the ordinary entry points, bit 1 the static scratch of
  * moa_decoder_feedforward_fp8_noalloc. Touches no device memory. */
 int moa_test_scratch_state(uint32_t* state);
+
+/* Test only: trips the state of `device` as a MOA_DEVERR_SPIN_TIMEOUT read by moa_device_errors
+ * does (no device needed), so the refusal path can be tested where no wait expires. */
+int moa_test_trip_device_state(int device);
 
 #ifdef __cplusplus
 }

@@ -2,6 +2,7 @@
 // and dispatch to the decode (small M) or chunk (large M) kernels.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -33,6 +34,29 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 }  // namespace
 
 int set_error(int code, const char* msg) { return fail(code, msg); }
+
+// Per device: a one-token call's bounded cross-workgroup wait expired (MOA_DEVERR_SPIN_TIMEOUT,
+// seen by moa_device_errors), so that call's outputs may be partly written. Until the caller
+// acknowledges it with moa_clear_device_state, every call that computes on that device and
+// moa_init refuse with MOA_ERROR_DEVICE_STATE instead of building on those outputs.
+namespace {
+std::atomic<uint32_t> g_tripped[kMaxDevices];
+
+// The current device's index for the tripped check; 0 when there is none (a failing HIP call
+// then reports the device problem itself).
+int current_device_or_0() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+    return dev;
+}
+
+int tripped_fail(int dev) {
+    return fail(MOA_ERROR_DEVICE_STATE,
+                "device " + std::to_string(dev) + ": a one-token call's cross-workgroup wait expired "
+                "(MOA_DEVERR_SPIN_TIMEOUT), so its outputs may be partly written; restore them, then call "
+                "moa_clear_device_state(" + std::to_string(dev) + ")");
+}
+}  // namespace
 
 DevCtx* existing_context(int dev) {
     std::lock_guard<std::mutex> lock(g_ctx_mutex);
@@ -133,6 +157,7 @@ DevCtx g_na_ctx[kMaxDevices];  // per device: pointers into that device's copy o
 // Once per device, with that device current: the device address of its `scratch`, carved into a
 // context of the layout above. Allocates nothing. nullptr (and *code set) on failure.
 DevCtx* noalloc_context(int* code) {
+    if (g_tripped[current_device_or_0()].load()) { *code = tripped_fail(current_device_or_0()); return nullptr; }
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) { *code = hip_fail(e, "hipGetDevice"); return nullptr; }
@@ -194,6 +219,7 @@ struct Check {
 };
 
 DevCtx* ctx_or_fail(int* code) {
+    if (g_tripped[current_device_or_0()].load()) { *code = tripped_fail(current_device_or_0()); return nullptr; }
     hipError_t e;
     DevCtx* c = device_context(&e);
     if (!c) *code = hip_fail(e, "allocating the per-device scratch");
@@ -317,6 +343,7 @@ const char* moa_version(void) { return "moa-gfx950 0.1.0"; }
 const char* moa_last_error_string(void) { return g_error.c_str(); }
 
 int moa_init(int device) {
+    if (device >= 0 && device < kMaxDevices && g_tripped[device].load()) return tripped_fail(device);
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     if (e != hipSuccess || n == 0) return fail(MOA_ERROR_NO_DEVICE, "no HIP device visible");
@@ -352,6 +379,13 @@ int moa_device_errors(void* stream, uint32_t* bits) {
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "reading device error bits");
     *bits = host[0] | host[1];
+    if (*bits & kErrSpinTimeout) g_tripped[dev].store(1u);
+    return MOA_SUCCESS;
+}
+
+int moa_clear_device_state(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(MOA_ERROR_INVALID_VALUE, "device index out of range");
+    g_tripped[device].store(0u);
     return MOA_SUCCESS;
 }
 
@@ -580,6 +614,7 @@ int moa_final_norm_and_logits(const uint16_t* input, const uint16_t* rms_weight,
     Check c;
     c.ptr(input, "input").ptr(rms_weight, "rms_weight").ptr(lm_head_weight, "lm_head_weight").ptr(out, "out").rows(M);
     if (c.code) return c.code;
+    if (g_tripped[current_device_or_0()].load()) return tripped_fail(current_device_or_0());
     return finish(launch_final_norm_and_logits(input, rms_weight, lm_head_weight, out, M, static_cast<hipStream_t>(stream)),
                   "final_norm_and_logits launch");
 }
@@ -591,6 +626,7 @@ int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* 
     if (c.code) return c.code;
     if (N < 1 || K < 16 || K % 16) return fail(MOA_ERROR_INVALID_VALUE, "need N >= 1 and K a positive multiple of 16");
     if (M > 65535) return fail(MOA_ERROR_INVALID_VALUE, "M must be <= 65535 for the projection");
+    if (g_tripped[current_device_or_0()].load()) return tripped_fail(current_device_or_0());
     ProjParams p{x, w, scale, ScaleKind::F32, out, N, K};
     return finish(launch_proj_decode(p, M, static_cast<hipStream_t>(stream)), "fp8_scaled_projection launch");
 }
@@ -670,6 +706,12 @@ int moa_test_take_overs(uint32_t* count) {
     }
     if (e == hipSuccess) *count = total;
     return finish(e, "reading the take-over count");
+}
+
+int moa_test_trip_device_state(int device) {
+    if (device < 0 || device >= kMaxDevices) return fail(MOA_ERROR_INVALID_VALUE, "device index out of range");
+    g_tripped[device].store(1u);
+    return MOA_SUCCESS;
 }
 
 int moa_test_scratch_state(uint32_t* state) {

@@ -82,6 +82,8 @@ SIGNATURES = {
     "moa_test_set_stall": [C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)],
     "moa_test_take_overs": [U32P],
     "moa_test_scratch_state": [U32P],
+    "moa_test_trip_device_state": [I32],
+    "moa_clear_device_state": [I32],
     # include/moa_bench.h
     "moa_bench_stream_read": [P, U64, I32, I32, P, P],
 }

@@ -9,15 +9,37 @@ stream). Tensors are torch tensors on a ROCm device:
   per-channel scales    torch.float32 (ops.rs uses bf16: pass torch.bfloat16 and the
                         exact bf16 entry point is used)
 
-Errors from the library raise MoaError; nothing falls back to a CPU path.
+Errors from the library raise MoaError; nothing falls back to a CPU path. In checked mode
+(set_checked(True), or MOA_CHECK_DEVICE_ERRORS=1 in the environment) every operator call is
+followed by device_errors(), which synchronises, and any device-side error bit raises MoaError
+(MOA_ERROR_DEVICE_STATE); off by default, since the check synchronises the stream.
 """
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import torch
 
 from . import _lib
+
+_checked = os.environ.get("MOA_CHECK_DEVICE_ERRORS", "") not in ("", "0")
+
+
+def set_checked(on: bool) -> None:
+    """Checked mode on or off (see the module docstring)."""
+    global _checked
+    _checked = bool(on)
+
+
+def _call(name: str, *args) -> None:
+    """One operator entry point; in checked mode, then the device's error bits."""
+    _lib.call(name, *args)
+    if _checked:
+        bits = device_errors()
+        if bits:
+            raise _lib.MoaError(-5, f"{name}: device error bits {bits:#x} (1 rope offset, 2 kv offset, "
+                                    f"4 expired wait: the device state is now tripped, see clear_device_state)")
 
 H, L, NS, GS, DS, QS, PS, TS, E, W = 3840, 15360, 8, 2, 256, 4096, 2048, 1024, 32768, 262144
 
@@ -91,7 +113,7 @@ def sliding_project_qkv(x, q_weight, k_weight, v_weight, q_weight_scale, k_weigh
         _ptr(q_out, "q_out", _BF16, M * QS),
     ]
     name = "moa_sliding_project_qkv_bf16_scales" if bf else "moa_sliding_project_qkv"
-    _lib.call(name, *args, M, _stream(x))
+    _call(name, *args, M, _stream(x))
 
 
 def sliding_attention(q, k, v, mask, out) -> None:
@@ -103,7 +125,7 @@ def sliding_attention(q, k, v, mask, out) -> None:
         _ptr(q, "q", _BF16), _ptr(k, "k", _BF16, TS * NS * DS), _ptr(v, "v", _BF16, TS * NS * DS),
         _ptr(mask, "mask", _F32, M * TS), _ptr(out, "out", _BF16, M * QS),
     ]
-    _lib.call("moa_sliding_attention", *args, M, _stream(q))
+    _call("moa_sliding_attention", *args, M, _stream(q))
 
 
 GF, DF, QF, PF, TF = 16, 512, 8192, 512, 512  # full-attention layers (FO/src/axes.rs)
@@ -123,7 +145,7 @@ def full_project_qkv(x, q_weight, k_weight, q_weight_scale, k_weight_scale, inpu
         _ptr(k_cache, "k_cache", _BF16, TF * DF), _ptr(v_cache, "v_cache", _BF16, TF * DF),
         _ptr(q_out, "q_out", _BF16, M * QF),
     ]
-    _lib.call("moa_full_project_qkv", *args, M, _stream(x))
+    _call("moa_full_project_qkv", *args, M, _stream(x))
 
 
 def _full_page(name, q, k, v, mask, running_max, running_sum, out):
@@ -133,7 +155,7 @@ def _full_page(name, q, k, v, mask, running_max, running_sum, out):
         _ptr(mask, "mask", _F32, M * TF), _ptr(running_max, "running_max", _F32, M * GF),
         _ptr(running_sum, "running_sum", _F32, M * GF), _ptr(out, "out", _BF16, M * QF),
     ]
-    _lib.call(name, *args, M, _stream(q))
+    _call(name, *args, M, _stream(q))
 
 
 def full_attention_first_page(q, k, v, mask, running_max, running_sum, out) -> None:
@@ -158,7 +180,7 @@ def full_attention(q, k_pages, v_pages, masks, running_max, running_sum, out) ->
     ]
     tail = [_ptr(running_max, "running_max", _F32, M * GF), _ptr(running_sum, "running_sum", _F32, M * GF),
             _ptr(out, "out", _BF16, M * QF)]
-    _lib.call("moa_full_attention", *args, P, *tail, M, _stream(q))
+    _call("moa_full_attention", *args, P, *tail, M, _stream(q))
 
 
 def full_attention_output(x, running_sum, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
@@ -170,7 +192,7 @@ def full_attention_output(x, running_sum, post_attn_rms_weight, o_weight, o_weig
         _ptr(post_attn_rms_weight, "post_attn_rms_weight", _BF16, H), _ptr(o_weight, "o_weight", _U8, H * QF),
         _ptr(o_weight_scale, "o_weight_scale", _BF16, H), _ptr(residual, "residual", _BF16, M * H),
     ]
-    _lib.call("moa_full_attention_output", *args, M, _stream(x))
+    _call("moa_full_attention_output", *args, M, _stream(x))
 
 
 def final_norm_and_logits(input, rms_weight, lm_head_weight, out) -> None:
@@ -181,7 +203,7 @@ def final_norm_and_logits(input, rms_weight, lm_head_weight, out) -> None:
         _ptr(input, "input", _BF16), _ptr(rms_weight, "rms_weight", _BF16, H),
         _ptr(lm_head_weight, "lm_head_weight", _BF16, W * H), _ptr(out, "out", _BF16, M * W),
     ]
-    _lib.call("moa_final_norm_and_logits", *args, M, _stream(input))
+    _call("moa_final_norm_and_logits", *args, M, _stream(input))
 
 
 def sliding_attention_output(x, post_attn_rms_weight, o_weight, o_weight_scale, residual) -> None:
@@ -194,7 +216,7 @@ def sliding_attention_output(x, post_attn_rms_weight, o_weight, o_weight_scale, 
         _ptr(residual, "residual", _BF16, M * H),
     ]
     name = "moa_sliding_attention_output_bf16_scales" if bf else "moa_sliding_attention_output"
-    _lib.call(name, *args, M, _stream(x))
+    _call(name, *args, M, _stream(x))
 
 
 def decoder_feedforward(residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed, down_weight_packed,
@@ -214,7 +236,7 @@ def decoder_feedforward(residual, pre_ff_rms_weight, up_weight_packed, gate_weig
         _ptr(down_global_scale, "down_global_scale", _F32, 1),
         _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
     ]
-    _lib.call("moa_decoder_feedforward", *args, M, _stream(residual))
+    _call("moa_decoder_feedforward", *args, M, _stream(residual))
 
 
 def decoder_feedforward_fp8(residual, pre_ff_rms_weight, up_weight, gate_weight, down_weight, up_weight_scale,
@@ -228,7 +250,7 @@ def decoder_feedforward_fp8(residual, pre_ff_rms_weight, up_weight, gate_weight,
         _ptr(gate_weight_scale, "gate_weight_scale", _F32, L), _ptr(down_weight_scale, "down_weight_scale", _F32, H),
         _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
     ]
-    _lib.call("moa_decoder_feedforward_fp8", *args, M, _stream(residual))
+    _call("moa_decoder_feedforward_fp8", *args, M, _stream(residual))
 
 
 def decoder_feedforward_mxfp4(residual, pre_ff_rms_weight, up_weight_packed, gate_weight_packed, down_weight_packed,
@@ -246,7 +268,7 @@ def decoder_feedforward_mxfp4(residual, pre_ff_rms_weight, up_weight_packed, gat
         _ptr(down_weight_scale, "down_weight_scale", _U8, H * L // 32),
         _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
     ]
-    _lib.call("moa_decoder_feedforward_mxfp4", *args, M, _stream(residual))
+    _call("moa_decoder_feedforward_mxfp4", *args, M, _stream(residual))
 
 
 def _o_args(x, post_attn_rms_weight, o_weight, o_weight_scale, residual, scale_dtypes):
@@ -279,7 +301,7 @@ def sliding_attention_output_feedforward(x, post_attn_rms_weight, o_weight, o_we
         _ptr(down_global_scale, "down_global_scale", _F32, 1),
         _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
     ]
-    _lib.call("moa_sliding_attention_output_feedforward", *args, M, _stream(x))
+    _call("moa_sliding_attention_output_feedforward", *args, M, _stream(x))
 
 
 def sliding_attention_output_feedforward_fp8(x, post_attn_rms_weight, o_weight, o_weight_scale, residual,
@@ -296,7 +318,7 @@ def sliding_attention_output_feedforward_fp8(x, post_attn_rms_weight, o_weight, 
         _ptr(gate_weight_scale, "gate_weight_scale", _F32, L), _ptr(down_weight_scale, "down_weight_scale", _F32, H),
         _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
     ]
-    _lib.call("moa_sliding_attention_output_feedforward_fp8", *args, M, _stream(x))
+    _call("moa_sliding_attention_output_feedforward_fp8", *args, M, _stream(x))
 
 
 def sliding_attention_output_feedforward_mxfp4(x, post_attn_rms_weight, o_weight, o_weight_scale, residual,
@@ -316,7 +338,7 @@ def sliding_attention_output_feedforward_mxfp4(x, post_attn_rms_weight, o_weight
         _ptr(down_weight_scale, "down_weight_scale", _U8, H * L // 32),
         _ptr(post_ff_rms_weight, "post_ff_rms_weight", _BF16, H), _ptr(layer_scalar, "layer_scalar", _BF16, 8),
     ]
-    _lib.call("moa_sliding_attention_output_feedforward_mxfp4", *args, M, _stream(x))
+    _call("moa_sliding_attention_output_feedforward_mxfp4", *args, M, _stream(x))
 
 
 def fp8_scaled_projection(x, w, scale, out) -> None:
@@ -325,7 +347,7 @@ def fp8_scaled_projection(x, w, scale, out) -> None:
     M = _rows(x, K, "x")
     args = [_ptr(x, "x", _BF16), _ptr(w, "w", _U8, N * K), _ptr(scale, "scale", _F32, N),
             _ptr(out, "out", _BF16, M * N)]
-    _lib.call("moa_fp8_scaled_projection", *args, M, N, K, _stream(x))
+    _call("moa_fp8_scaled_projection", *args, M, N, K, _stream(x))
 
 
 def device_errors(device: torch.device | None = None) -> int:
@@ -336,6 +358,11 @@ def device_errors(device: torch.device | None = None) -> int:
         s = torch.cuda.current_stream().cuda_stream
         _lib.call("moa_device_errors", C.c_void_p(s), C.byref(bits))
     return int(bits.value)
+
+
+def clear_device_state(device: int = 0) -> None:
+    """moa_clear_device_state: acknowledge a tripped device (an expired wait's outputs restored)."""
+    _lib.call("moa_clear_device_state", device)
 
 
 def format_selftest(device="cuda") -> torch.Tensor:
