@@ -106,7 +106,7 @@ def main() -> int:
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
                                           "ffn_mxfp4", "ffn_mxfp4_m16", "o_ffn",
-                             "chunk", "floor"), default=None,
+                             "chunk", "chunk_o_ffn", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     ap.add_argument("--floor-shapes", action="store_true",
@@ -239,6 +239,15 @@ def main() -> int:
         run_co(i)
         run_cffn(i)
 
+    def run_layer_o_ffn(i):
+        # the same layer with O and the FFN through one entry point (O's post rows also write the
+        # FFN's normalised input)
+        run_cqkv(i)
+        v, w = OW[i % no], FW[i % nf]
+        ops.sliding_attention_output_feedforward_fp8(
+            c_attn, o_post, v["o_weight"], v["o_weight_scale"], c_res, f_pre, w["up_weight"], w["gate_weight"],
+            w["down_weight"], w["up_weight_scale"], w["gate_weight_scale"], w["down_weight_scale"], f_post, f_ls)
+
     if CM:
         c_res_mx = dev(synth.bf16_normal("cfg4.mxfp4.residual", (CM, 3840)))
 
@@ -361,7 +370,8 @@ def main() -> int:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
               "fattn_fused64": run_fattn_fused64, "fo": run_fo, "ffn_mxfp4": run_ffn_mxfp4,
-              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer, "o_ffn": run_o_ffn}[args.profile]
+              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer, "chunk_o_ffn": run_layer_o_ffn,
+              "o_ffn": run_o_ffn}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -403,9 +413,9 @@ def main() -> int:
     if CM:
         chunk = {"rows": CM, "peak_TFLOPs": MFMA_BF16_PEAK_TFLOPS, "peak_fp8_TFLOPs": MFMA_FP8_PEAK_TFLOPS, "ops": {}}
         for name, fn in (("qkv", run_cqkv), ("o", run_co), ("ffn", run_cffn), ("layer", run_layer),
-                         ("ffn_mxfp4", run_cffn_mxfp4)):
+                         ("layer_o_ffn", run_layer_o_ffn), ("ffn_mxfp4", run_cffn_mxfp4)):
             ms, p10, p90 = graph_stats(fn, calls=8, warmup=8, replays=10)
-            flops = CM * (sum(FLOPS_PER_ROW.values()) if name == "layer" else FLOPS_PER_ROW[name.split("_")[0]])
+            flops = CM * (sum(FLOPS_PER_ROW.values()) if name.startswith("layer") else FLOPS_PER_ROW[name.split("_")[0]])
             tf = flops / (ms * 1e-3) / 1e12
             chunk["ops"][name] = {"us": round(ms * 1e3, 2), "us_p10": round(p10 * 1e3, 2), "us_p90": round(p90 * 1e3, 2),
                                   "us_per_token": round(ms * 1e3 / CM, 4), "TFLOPs": round(tf, 1),

@@ -330,6 +330,14 @@ int o_ffn_common(const OParams& o, const FfnParams& p, int M, void* stream) {
     hipError_t e = hipSuccess;
     if (M == 1 && launch_o_ffn_fused(o, p, s, ctx, &e))
         return finish(e, "sliding_attention_output_feedforward launch");
+    if (M > kMaxDecodeM) {  // the MFMA path: O's post rows write the FFN's normalised input too
+        for (int m0 = 0; m0 < M; m0 += kMaxChunkM) {
+            const int bad = finish(launch_o_ffn_chunk(o, p, m0, M - m0 < kMaxChunkM ? M - m0 : kMaxChunkM, s, ctx),
+                                   "sliding_attention_output_feedforward launch");
+            if (bad) return bad;
+        }
+        return MOA_SUCCESS;
+    }
     if (const int bad = o_launch(o, M, s, ctx)) return bad;
     return ffn_launch(p, M, s, ctx);
 }

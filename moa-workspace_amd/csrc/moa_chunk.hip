@@ -497,20 +497,13 @@ __device__ __forceinline__ float ck_block_sum(float v, float* red) {
 // out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) (gemma4.py:83-89), written as A tiles
 // (Tiles) or row-major [M][kH]. One workgroup per row (for tiles, row tile_row(b)); thread t < 240
 // owns elements 16t .. 16t+15.
-template <bool Tiles = true>
-__global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint16_t* __restrict__ x,
-                                                                      const uint16_t* __restrict__ w,
-                                                                      uint16_t* __restrict__ out) {
-    __shared__ float red[4];
-    const int t = threadIdx.x, m = Tiles ? tile_row(blockIdx.x, gridDim.x) : blockIdx.x;
+// Row m's norm from thread t's 16 elements xv (16t .. 16t+15, t < 240) and weights wv, stored.
+template <bool Tiles>
+__device__ __forceinline__ void rms_row_store(const float (&xv)[16], const float (&wv)[16], int m, float* red,
+                                              uint16_t* __restrict__ out) {
+    const int t = threadIdx.x;
     const bool act = t < kH / 16;
     const int c = min(t, kH / 16 - 1);
-    const uint16_t* xr = x + (size_t)m * kH + c * 16;
-    float xv[16], wv[16];
-    bf16x8_to_f32(ld16(xr), xv);
-    bf16x8_to_f32(ld16(xr + 8), xv + 8);
-    bf16x8_to_f32(ld16(w + c * 16), wv);
-    bf16x8_to_f32(ld16(w + c * 16 + 8), wv + 8);
     float ss = 0.0f;
     if (act) {
 #pragma unroll
@@ -526,6 +519,22 @@ __global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint
     const size_t o1 = Tiles ? atile_off(m, c * 16 + 8, kH) : (size_t)m * kH + c * 16 + 8;
     *reinterpret_cast<uint4*>(out + o0) = make_uint4(h[0], h[1], h[2], h[3]);
     *reinterpret_cast<uint4*>(out + o1) = make_uint4(h[4], h[5], h[6], h[7]);
+}
+
+template <bool Tiles = true>
+__global__ __launch_bounds__(kCkBlock) void chunk_rmsnorm_rows_kernel(const uint16_t* __restrict__ x,
+                                                                      const uint16_t* __restrict__ w,
+                                                                      uint16_t* __restrict__ out) {
+    __shared__ float red[4];
+    const int t = threadIdx.x, m = Tiles ? tile_row(blockIdx.x, gridDim.x) : blockIdx.x;
+    const int c = min(t, kH / 16 - 1);
+    const uint16_t* xr = x + (size_t)m * kH + c * 16;
+    float xv[16], wv[16];
+    bf16x8_to_f32(ld16(xr), xv);
+    bf16x8_to_f32(ld16(xr + 8), xv + 8);
+    bf16x8_to_f32(ld16(w + c * 16), wv);
+    bf16x8_to_f32(ld16(w + c * 16 + 8), wv + 8);
+    rms_row_store<Tiles>(xv, wv, m, red, out);
 }
 
 // Row-major bf16 [M][K] -> A tiles (the O-projection's input arrives row-major). One workgroup
@@ -662,13 +671,13 @@ __global__ __launch_bounds__(kCkBlock) void chunk_qkv_heads4_kernel(QkvParams p,
 // with N the post-RMSNorm (identity when w_post is null) and ls skipped when null
 // (shared/rmsnorm.rs:204-296, residual.rs:189-241; generate_references.py:411-413).
 // ZS: the most splits a call may have (the loads of all of them are in flight at once).
-template <ScaleKind SK, FfnFormat F = FfnFormat::FP8, int ZS = kCkSplitMax>
-__global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* __restrict__ part, int splits, int M,
-                                                                   const void* scale, const float* __restrict__ gscale,
-                                                                   const uint16_t* __restrict__ w_post,
-                                                                   uint16_t* __restrict__ res, const uint16_t* __restrict__ ls) {
-    __shared__ float red[4];
-    const int t = threadIdx.x, m = blockIdx.x;
+// Row m; out[i] returns thread t's stored chunk t + 256 i (8 bf16 values) of the new residual.
+template <ScaleKind SK, FfnFormat F, int ZS>
+__device__ __forceinline__ void post_row(const float* __restrict__ part, int splits, int M, const void* scale,
+                                         const float* __restrict__ gscale, const uint16_t* __restrict__ w_post,
+                                         uint16_t* __restrict__ res, const uint16_t* __restrict__ ls, int m, float* red,
+                                         uint4 (&out)[2]) {
+    const int t = threadIdx.x;
     const float gs = F == FfnFormat::NVFP4 ? *gscale : 1.0f;
     constexpr int NC = kH / 8;  // 480 chunks of 8; thread t owns t and t + 256
     float d[2][8];
@@ -731,8 +740,51 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
             const uint32_t b = f2bf(sres);
             if (e & 1) pk[e >> 1] |= b << 16; else pk[e >> 1] = b;
         }
-        *reinterpret_cast<uint4*>(rr) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        out[i] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *reinterpret_cast<uint4*>(rr) = out[i];
     }
+}
+
+template <ScaleKind SK, FfnFormat F = FfnFormat::FP8, int ZS = kCkSplitMax>
+__global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* __restrict__ part, int splits, int M,
+                                                                   const void* scale, const float* __restrict__ gscale,
+                                                                   const uint16_t* __restrict__ w_post,
+                                                                   uint16_t* __restrict__ res, const uint16_t* __restrict__ ls) {
+    __shared__ float red[4];
+    uint4 out[2];
+    post_row<SK, F, ZS>(part, splits, M, scale, gscale, w_post, res, ls, blockIdx.x, red, out);
+}
+
+// O's post rows with the FFN's pre-norm behind them (sliding_attention_output then
+// decoder_feedforward on one residual, FO/src/host/runtime.rs:440-459 then 543-571): row
+// tile_row(b) gets O's post-norm and residual as chunk_post_rows_kernel computes them, then the
+// FFN's pre-norm of the new residual, written as A tiles into hout exactly as
+// chunk_rmsnorm_rows_kernel<true> writes them (the row through LDS, so that thread t < 240 sums
+// elements 16t .. 16t+15 in the same order). The FFN then starts at its GEMM.
+template <ScaleKind SK, int ZS>
+__global__ __launch_bounds__(kCkBlock) void chunk_post_pre_rows_kernel(const float* __restrict__ part, int splits, int M,
+                                                                       const void* scale,
+                                                                       const uint16_t* __restrict__ w_post,
+                                                                       uint16_t* __restrict__ res,
+                                                                       const uint16_t* __restrict__ w_pre,
+                                                                       uint16_t* __restrict__ hout) {
+    __shared__ float red[4];
+    __shared__ __attribute__((aligned(16))) uint16_t row[kH];
+    const int t = threadIdx.x, m = tile_row(blockIdx.x, gridDim.x);
+    const int c = min(t, kH / 16 - 1);
+    float wv[16];
+    bf16x8_to_f32(ld16(w_pre + c * 16), wv);
+    bf16x8_to_f32(ld16(w_pre + c * 16 + 8), wv + 8);
+    uint4 out[2];
+    post_row<SK, FfnFormat::FP8, ZS>(part, splits, M, scale, nullptr, w_post, res, nullptr, m, red, out);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (t + 256 * i < kH / 8) *reinterpret_cast<uint4*>(row + (t + 256 * i) * 8) = out[i];
+    __syncthreads();
+    float xv[16];
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(row + c * 16), xv);
+    bf16x8_to_f32(*reinterpret_cast<const uint4*>(row + c * 16 + 8), xv + 8);
+    rms_row_store<true>(xv, wv, m, red, hout);
 }
 
 template <typename K, typename... A>
@@ -836,10 +888,12 @@ hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx
         : post_rows<ScaleKind::BF16>(ctx->fbuf, sp, M, p.os, p.post_rms, res, nullptr, s);
 }
 
+// normed: the pre-norm's A tiles are already in ctx->hbuf (o_ffn_chunk)
 template <FfnFormat F>
-hipError_t ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+hipError_t ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed = false) {
     uint16_t* res = p.residual + (size_t)m0 * kH;
-    hipError_t e = ck_launch(chunk_rmsnorm_rows_kernel<true>, dim3(M), s, (const uint16_t*)res, p.pre_rms, ctx->hbuf);
+    hipError_t e = normed ? hipSuccess
+                          : ck_launch(chunk_rmsnorm_rows_kernel<true>, dim3(M), s, (const uint16_t*)res, p.pre_rms, ctx->hbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
     g.x = ctx->hbuf; g.M = M; g.N = kL; g.K = kH;
@@ -864,6 +918,38 @@ hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, De
         case FfnFormat::FP8: return ffn_chunk<FfnFormat::FP8>(p, m0, M, s, ctx);
         case FfnFormat::NVFP4: return ffn_chunk<FfnFormat::NVFP4>(p, m0, M, s, ctx);
         case FfnFormat::MXFP4: return ffn_chunk<FfnFormat::MXFP4>(p, m0, M, s, ctx);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_o_ffn_chunk(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    if (o.residual != p.residual) return hipErrorInvalidValue;
+    hipError_t e = ck_launch(chunk_tile_rows_kernel, dim3(M), s, o.x + (size_t)m0 * kQs, kQs, ctx->pbuf);
+    if (e != hipSuccess) return e;
+    GemmArgs g{};
+    g.x = ctx->pbuf; g.M = M; g.N = kH; g.K = kQs;
+    g.w[0] = o.ow; g.nseg[0] = 0; g.nseg[1] = kH; g.nsegs = 1;
+    g.yf = ctx->fbuf;
+    const int sp = pick_splits(kH / kCkOBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
+    e = gemm_partial<FfnFormat::FP8, kCkOBN>(g, sp, o.scale_kind, s);
+    if (e != hipSuccess) return e;
+    uint16_t* res = o.residual + (size_t)m0 * kH;
+    const float* part = ctx->fbuf;
+    if (o.scale_kind == ScaleKind::F32)
+        e = sp <= 4 ? ck_launch(chunk_post_pre_rows_kernel<ScaleKind::F32, 4>, dim3(M), s, part, sp, M, o.os, o.post_rms,
+                                res, p.pre_rms, ctx->hbuf)
+                    : ck_launch(chunk_post_pre_rows_kernel<ScaleKind::F32, kCkSplitMax>, dim3(M), s, part, sp, M, o.os,
+                                o.post_rms, res, p.pre_rms, ctx->hbuf);
+    else
+        e = sp <= 4 ? ck_launch(chunk_post_pre_rows_kernel<ScaleKind::BF16, 4>, dim3(M), s, part, sp, M, o.os, o.post_rms,
+                                res, p.pre_rms, ctx->hbuf)
+                    : ck_launch(chunk_post_pre_rows_kernel<ScaleKind::BF16, kCkSplitMax>, dim3(M), s, part, sp, M, o.os,
+                                o.post_rms, res, p.pre_rms, ctx->hbuf);
+    if (e != hipSuccess) return e;
+    switch (p.fmt) {
+        case FfnFormat::FP8: return ffn_chunk<FfnFormat::FP8>(p, m0, M, s, ctx, true);
+        case FfnFormat::NVFP4: return ffn_chunk<FfnFormat::NVFP4>(p, m0, M, s, ctx, true);
+        case FfnFormat::MXFP4: return ffn_chunk<FfnFormat::MXFP4>(p, m0, M, s, ctx, true);
     }
     return hipErrorInvalidValue;
 }

@@ -166,6 +166,8 @@ hipError_t launch_full_attention(const uint16_t* q, const uint16_t* k_pages, con
 hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);  // every format
+// sliding_attention_output then decoder_feedforward on one residual (o.residual == p.residual)
+hipError_t launch_o_ffn_chunk(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 // decoder_feedforward for 1..kMaxDecodeM rows on the matrix cores (every format; moa_rows.hip), and its
 // last step: the sum of `splits` f32 partials [splits][M][kH] of the down projection, the format's
 // commit, post-RMSNorm, residual and layer scalar into res [M][kH].

@@ -155,3 +155,33 @@ def test_interleaved_with_the_ffn_entry_point():
     for i in range(3):
         assert np.array_equal(gpu_fused("fp8", o, f), want), f"fused call {i}"
         assert np.array_equal(gpu_fp8(f), ffn_want), f"ffn call {i}"
+
+
+def chunk_inputs(fmt, M):
+    """O inputs of M rows and FFN weights of `fmt` with their own M-row residual (O's is unused:
+    the call runs on one residual, the FFN's)."""
+    o = synth.cfg_o(3, M=M, tag="offn_chunk")
+    if fmt == "fp8":
+        f = synth.cfg_ffn_fp8(3, M=M, tag="offn_chunk")
+    else:
+        f = dict(synth.cfg_ffn_mxfp4(3) if fmt == "mxfp4" else synth.ref_ffn_inputs(3))
+        f["residual"] = synth.bf16_normal(f"offn_chunk.{fmt}.M{M}.residual", (M, 3840))
+    o["residual"] = f["residual"].copy()
+    return o, f
+
+
+@pytest.mark.parametrize("fmt,M", [("fp8", 17), ("fp8", 100), ("fp8", 300), ("mxfp4", 256), ("nvfp4", 64)])
+def test_chunk_rows_write_the_ffn_input_with_the_o_post_norm(fmt, M):
+    """More than 16 rows take the MFMA path, where O's post rows also write the FFN's normalised
+    input (chunk_post_pre_rows_kernel) and the FFN starts at its GEMM: the same bits as the two
+    calls (whose MFMA path runs the FFN's own norm kernel), and the oracle's chain within the gate."""
+    need_gpu()
+    say(f"o->ffn {fmt} M{M} (MFMA path)")
+    o, f = chunk_inputs(fmt, M)
+    got = gpu_fused(fmt, o, f)
+    two = gpu_two_calls(fmt, o, f)
+    diff = np.count_nonzero(got.reshape(-1) != two.reshape(-1))
+    say(f"[o->ffn {fmt} M{M}] fused vs two calls: {diff} of {got.size} differ")
+    assert diff == 0
+    if M <= 100:
+        gate(oracle_chain(fmt, o, f), got, f"o->ffn {fmt} M{M}", atol=FFN_ATOL)
