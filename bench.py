@@ -79,7 +79,7 @@ BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          "fattn_fused": FATTN_PAGES * (2 * 512 * 512 * 2 + 512 * 4) + 8192 * 2 * 2 + 16 * 4 * 2,
          # the same at the cache's full 64 pages (position 32767)
          "fattn_fused64": 64 * (2 * 512 * 512 * 2 + 512 * 4) + 8192 * 2 * 2 + 16 * 4 * 2}
-GRAPH_CALLS = 40  # calls per captured graph
+GRAPH_CALLS = 200  # calls per captured graph (as many as the headline step's K)
 REPLAYS = 20  # timed replays per graph (median, p10, p90 over them)
 # Config 4 (MFMA path): flops per token row; the MFMA runs bf16 x bf16 (FP8 weights widen exactly).
 FLOPS_PER_ROW = {"qkv": 2 * 3840 * 8192, "o": 2 * 4096 * 3840, "ffn": 3 * 2 * 3840 * 15360}
@@ -342,7 +342,9 @@ def main() -> int:
         """Graph-driven: `calls` consecutive calls (cycling the weight copies) captured once in a
         HIP graph; warm-up replays covering `warmup` calls, then `replays` replays back to back with
         an event between consecutive ones on the replay stream. Returns the median, p10 and p90 of
-        ms per call over the replays."""
+        ms per call over the replays. At least two warm-up replays: the first replays after a
+        capture run slow (measured on the FFN with 40-call graphs: the first 8 of 20 replays 2-5 %
+        slower than the rest; with 200-call graphs only the first)."""
         for i in range(3):
             fn(i)
         torch.cuda.synchronize()
@@ -350,7 +352,7 @@ def main() -> int:
         with torch.cuda.graph(g):
             for i in range(calls):
                 fn(i)
-        for _ in range(max(1, math.ceil(warmup / calls))):
+        for _ in range(max(2, math.ceil(warmup / calls))):
             g.replay()
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
@@ -569,6 +571,7 @@ def floor_measure(torch, np, sweep: bool = False):
         with torch.cuda.graph(g):
             for i in range(calls):
                 fn(i)
+        g.replay()
         g.replay()
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(REPLAYS + 1)]
