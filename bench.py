@@ -106,7 +106,7 @@ def main() -> int:
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
                                           "ffn_mxfp4", "ffn_mxfp4_m16", "o_ffn",
-                             "chunk", "chunk_o_ffn", "floor"), default=None,
+                                          "chunk", "chunk_o_ffn", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
     ap.add_argument("--floor-shapes", action="store_true",
@@ -288,6 +288,14 @@ def main() -> int:
         w = AW[i % na]
         ops.sliding_attention(a_q, w["k_cache"], w["v_cache"], a_mask, a_out)
 
+    def run_qkv_then_attn(i):
+        # QKV writes its slot into the attention's rotated caches and the attention reads them
+        w, c = QW[i % nq], AW[i % na]
+        ops.sliding_project_qkv(q["x"], w["q_weight"], w["k_weight"], w["v_weight"], w["q_weight_scale"],
+                                w["k_weight_scale"], w["v_weight_scale"], q["input_rms_weight"], q["q_rms_weight"],
+                                q["k_rms_weight"], kv, ro, q["cos"], q["sin"], c["k_cache"], c["v_cache"], q_out)
+        ops.sliding_attention(q_out, c["k_cache"], c["v_cache"], a_mask, a_out)
+
     def run_fqkv(i):
         w = FQW[i % nfq]
         ops.full_project_qkv(fq_d["x"], w["q_weight"], w["k_weight"], w["q_weight_scale"], w["k_weight_scale"],
@@ -320,6 +328,15 @@ def main() -> int:
         run_qkv(i)
         run_o(i)
         run_ffn(i)
+
+    def run_layer_calls(i):  # the sliding layer's decode step as the runtime calls it: four operators
+        run_qkv_then_attn(i)
+        run_o(i)
+        run_ffn(i)
+
+    def run_layer_fused(i):  # the same with O and the FFN in one launch: three launches
+        run_qkv_then_attn(i)
+        run_o_ffn(i)
 
     def run_step_fused(i):
         run_qkv(i)
@@ -410,6 +427,10 @@ def main() -> int:
     # the same step with O and the FFN in one launch (moa_sliding_attention_output_feedforward_fp8)
     ms_fstep, fstep_p10, fstep_p90 = graph_stats(run_step_fused, calls=args.steps, warmup=max(args.warmup, 1))
     log(f"step, O->FFN fused {ms_fstep * 1e3:9.2f} us/token [p10 {fstep_p10 * 1e3:.2f}, p90 {fstep_p90 * 1e3:.2f}]")
+    # the whole sliding-layer step (attention included): four calls, and three launches
+    ms_lc, lc_p10, lc_p90 = graph_stats(run_layer_calls, calls=args.steps, warmup=max(args.warmup, 1))
+    ms_lf, lf_p10, lf_p90 = graph_stats(run_layer_fused, calls=args.steps, warmup=max(args.warmup, 1))
+    log(f"layer step: four calls {ms_lc * 1e3:9.2f} us, three launches {ms_lf * 1e3:9.2f} us")
 
     chunk = None
     if CM:
@@ -474,6 +495,12 @@ def main() -> int:
                              "us_p90": round(fstep_p90 * 1e3, 3),
                              "workload": "sliding_project_qkv (cfg2) + sliding_attention_output_feedforward_fp8 "
                                          "(cfg1 then cfg0, one launch)"},
+        "layer_step": {"us_four_calls": round(ms_lc * 1e3, 3), "us_four_calls_p90": round(lc_p90 * 1e3, 3),
+                       "us_three_launches": round(ms_lf * 1e3, 3), "us_three_launches_p90": round(lf_p90 * 1e3, 3),
+                       "workload": "the sliding layer's decode step with its attention (pos 5000, all 1024 "
+                                   "slots): sliding_project_qkv, sliding_attention, sliding_attention_output, "
+                                   "decoder_feedforward_fp8 as four calls, and with the last two through "
+                                   "sliding_attention_output_feedforward_fp8 (one launch)"},
         "floor": floor,
         "us_per_token_host_driven": round(ms_step_host * 1e3, 3),
         "hbm_copy_GBps": round(copy_gbps, 1),
