@@ -170,7 +170,9 @@ def chunk_inputs(fmt, M):
     return o, f
 
 
-@pytest.mark.parametrize("fmt,M", [("fp8", 17), ("fp8", 100), ("fp8", 300), ("mxfp4", 256), ("nvfp4", 64)])
+# 1030 rows: two chunks of the MFMA path (1024 rows each at most), the second of 6 rows
+@pytest.mark.parametrize("fmt,M", [("fp8", 17), ("fp8", 100), ("fp8", 300), ("mxfp4", 256), ("nvfp4", 64),
+                                   ("fp8", 1030)])
 def test_chunk_rows_write_the_ffn_input_with_the_o_post_norm(fmt, M):
     """More than 16 rows take the MFMA path, where O's post rows also write the FFN's normalised
     input (chunk_post_pre_rows_kernel) and the FFN starts at its GEMM: the same bits as the two
