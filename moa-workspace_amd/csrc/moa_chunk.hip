@@ -872,15 +872,21 @@ hipError_t launch_qkv_chunk(const QkvParams& p, int m0, int M, hipStream_t s, De
         : ck_launch(chunk_qkv_heads4_kernel<ScaleKind::BF16, 4>, dim3(8, M), s, p, m0, M, part, sp, ctx->err);
 }
 
-hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+// O's A tiles and its split-K GEMM into ctx->fbuf; *sp: the splits
+static hipError_t o_chunk_gemm(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, int* sp) {
     hipError_t e = ck_launch(chunk_tile_rows_kernel, dim3(M), s, p.x + (size_t)m0 * kQs, kQs, ctx->pbuf);
     if (e != hipSuccess) return e;
     GemmArgs g{};
     g.x = ctx->pbuf; g.M = M; g.N = kH; g.K = kQs;
     g.w[0] = p.ow; g.nseg[0] = 0; g.nseg[1] = kH; g.nsegs = 1;
     g.yf = ctx->fbuf;
-    const int sp = pick_splits(kH / kCkOBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
-    e = gemm_partial<FfnFormat::FP8, kCkOBN>(g, sp, p.scale_kind, s);
+    *sp = pick_splits(kH / kCkOBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
+    return gemm_partial<FfnFormat::FP8, kCkOBN>(g, *sp, p.scale_kind, s);
+}
+
+hipError_t launch_o_chunk(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    int sp = 1;
+    const hipError_t e = o_chunk_gemm(p, m0, M, s, ctx, &sp);
     if (e != hipSuccess) return e;
     uint16_t* res = p.residual + (size_t)m0 * kH;
     return p.scale_kind == ScaleKind::F32
@@ -924,14 +930,8 @@ hipError_t launch_ffn_chunk(const FfnParams& p, int m0, int M, hipStream_t s, De
 
 hipError_t launch_o_ffn_chunk(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
     if (o.residual != p.residual) return hipErrorInvalidValue;
-    hipError_t e = ck_launch(chunk_tile_rows_kernel, dim3(M), s, o.x + (size_t)m0 * kQs, kQs, ctx->pbuf);
-    if (e != hipSuccess) return e;
-    GemmArgs g{};
-    g.x = ctx->pbuf; g.M = M; g.N = kH; g.K = kQs;
-    g.w[0] = o.ow; g.nseg[0] = 0; g.nseg[1] = kH; g.nsegs = 1;
-    g.yf = ctx->fbuf;
-    const int sp = pick_splits(kH / kCkOBN * m_tiles(M), kQs / kCkBK, (size_t)M * kH);
-    e = gemm_partial<FfnFormat::FP8, kCkOBN>(g, sp, o.scale_kind, s);
+    int sp = 1;
+    hipError_t e = o_chunk_gemm(o, m0, M, s, ctx, &sp);
     if (e != hipSuccess) return e;
     uint16_t* res = o.residual + (size_t)m0 * kH;
     const float* part = ctx->fbuf;
