@@ -65,6 +65,11 @@ BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          # weights once, plus the rows' residual read and write, the two norm weights, the layer scalar
          "ffn_mxfp4": 94_003_200 + 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
          "ffn_mxfp4_m16": 94_003_200 + 16 * 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
+         # O at 16 rows (15 more input rows and residual rows read and written), and O then the
+         # MXFP4 FFN on those 16 residual rows through one entry point (less the rows between them)
+         "o_m16": 15_775_232 + 15 * (4096 * 2 + 2 * 3840 * 2),
+         "o_ffn_mxfp4_m16": 15_775_232 + 15 * (4096 * 2 + 2 * 3840 * 2) + 94_003_200 + 16 * 2 * 3840 * 2
+                            + 2 * 3840 * 2 + 16 - 16 * 2 * 3840 * 2,
          # sliding_attention, all 1024 slots valid: K and V caches + q + out + mask row
          "attn": 2 * 1024 * 8 * 256 * 2 + 2 * 4096 * 2 + 1024 * 4,
          # final_norm_and_logits: the bf16 lm_head (262144 x 3840) + input + norm weight + logits
@@ -105,7 +110,7 @@ def main() -> int:
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
-                                          "ffn_mxfp4", "ffn_mxfp4_m16", "o_ffn",
+                                          "ffn_mxfp4", "ffn_mxfp4_m16", "o_ffn", "o_m16", "o_ffn_mxfp4_m16",
                                           "chunk", "chunk_o_ffn", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
@@ -197,6 +202,7 @@ def main() -> int:
     MXW = replicate(mx, MXK, nmx)
     mx_res16 = dev(mx["residual"])
     mx_res1 = mx_res16[:1].clone()
+    o_x16 = dev(synth.bf16_normal("bench.o.x16", (16, 4096)))  # 16 attention rows for O at M = 16
     o_x, o_post, o_res = dev(o["x"]), dev(o["post_attn_rms_weight"]), dev(o["residual"])
     q = {k: dev(qkv[k]) for k in ("x", "input_rms_weight", "q_rms_weight", "k_rms_weight", "cos", "sin",
                                   "k_cache", "v_cache")}
@@ -271,6 +277,17 @@ def main() -> int:
     def run_o(i):
         w = OW[i % no]
         ops.sliding_attention_output(o_x, o_post, w["o_weight"], w["o_weight_scale"], o_res)
+
+    def run_o_m16(i):
+        w = OW[i % no]
+        ops.sliding_attention_output(o_x16, o_post, w["o_weight"], w["o_weight_scale"], mx_res16)
+
+    def run_o_ffn_mxfp4_m16(i):
+        # 16 rows of O then the MXFP4 FFN through one entry point (the rows path: O's post rows
+        # also write the FFN's normalised input)
+        v, w = OW[i % no], MXW[i % nmx]
+        ops.sliding_attention_output_feedforward_mxfp4(o_x16, o_post, v["o_weight"], v["o_weight_scale"], mx_res16,
+                                                       f_pre, *[w[k] for k in MXK], f_post, f_ls)
 
     def run_o_ffn(i):
         v, w = OW[i % no], FW[i % nf]
@@ -390,7 +407,7 @@ def main() -> int:
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
               "fattn_fused64": run_fattn_fused64, "fo": run_fo, "ffn_mxfp4": run_ffn_mxfp4,
               "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer, "chunk_o_ffn": run_layer_o_ffn,
-              "o_ffn": run_o_ffn}[args.profile]
+              "o_ffn": run_o_ffn, "o_m16": run_o_m16, "o_ffn_mxfp4_m16": run_o_ffn_mxfp4_m16}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -406,7 +423,8 @@ def main() -> int:
 
     per_op = {}
     for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("o_ffn", run_o_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
-                     ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("attn", run_attn), ("logits", run_logits),
+                     ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("o_m16", run_o_m16), ("o_ffn_mxfp4_m16", run_o_ffn_mxfp4_m16),
+                     ("attn", run_attn), ("logits", run_logits),
                      ("fqkv", run_fqkv), ("fattn", run_fattn), ("fattn_fused", run_fattn_fused),
                      ("fattn_fused64", run_fattn_fused64), ("fo", run_fo)):
         ms, p10, p90 = graph_stats(fn, replays=5 if name == "logits" else REPLAYS)

@@ -187,7 +187,7 @@ int moa_decoder_feedforward_mxfp4(uint16_t* residual, const uint16_t* pre_ff_rms
  * NVFP4 FFN weights). Arguments are those of moa_sliding_attention_output_bf16_scales followed by
  * those of moa_decoder_feedforward after its residual. The residual afterwards has the same bits
  * as those two calls made in turn; at M = 1 it is one launch (the residual between the two
- * operators is never written to memory), and above 16 rows O's last kernel also writes the FFN's
+ * operators is never written to memory), and from 3 rows on O's last kernel also writes the FFN's
  * normalised input (one kernel fewer). */
 int moa_sliding_attention_output_feedforward(
     const uint16_t* x, const uint16_t* post_attn_rms_weight, const uint8_t* o_weight, const uint16_t* o_weight_scale,

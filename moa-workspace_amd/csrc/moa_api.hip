@@ -319,7 +319,9 @@ int ffn_common(const FfnParams& p, int M, void* stream) {
 }
 
 // sliding_attention_output then decoder_feedforward on one residual: one launch for a token row
-// when a single-launch kernel covers the operand types, else the two operators in turn.
+// when a single-launch kernel covers the operand types; from kRowsProjMinM rows on, O's last row
+// kernel also writes the FFN's normalised input (one kernel fewer than the two operators); else
+// (two rows) the two operators in turn.
 int o_ffn_common(const OParams& o, const FfnParams& p, int M, void* stream) {
     if (const int bad = o_check(o, M)) return bad;
     if (const int bad = ffn_check(p, M)) return bad;
@@ -338,6 +340,8 @@ int o_ffn_common(const OParams& o, const FfnParams& p, int M, void* stream) {
         }
         return MOA_SUCCESS;
     }
+    if (M >= kRowsProjMinM)  // the rows path: O's post rows write the FFN's normalised input too
+        return finish(launch_o_ffn_rows(o, p, 0, M, s, ctx), "sliding_attention_output_feedforward launch");
     if (const int bad = o_launch(o, M, s, ctx)) return bad;
     return ffn_launch(p, M, s, ctx);
 }

@@ -756,12 +756,13 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_rows_kernel(const float* 
 }
 
 // O's post rows with the FFN's pre-norm behind them (sliding_attention_output then
-// decoder_feedforward on one residual, FO/src/host/runtime.rs:440-459 then 543-571): row
-// tile_row(b) gets O's post-norm and residual as chunk_post_rows_kernel computes them, then the
-// FFN's pre-norm of the new residual, written as A tiles into hout exactly as
-// chunk_rmsnorm_rows_kernel<true> writes them (the row through LDS, so that thread t < 240 sums
-// elements 16t .. 16t+15 in the same order). The FFN then starts at its GEMM.
-template <ScaleKind SK, int ZS>
+// decoder_feedforward on one residual, FO/src/host/runtime.rs:440-459 then 543-571): a row gets
+// O's post-norm and residual as chunk_post_rows_kernel computes them, then the FFN's pre-norm of
+// the new residual, written into hout exactly as chunk_rmsnorm_rows_kernel<Tiles> writes it (the
+// row through LDS, so that thread t < 240 sums elements 16t .. 16t+15 in the same order): A tiles
+// for the MFMA GEMMs (row tile_row(b)), row-major for the rows path (row b). The FFN then starts
+// at its first projection.
+template <ScaleKind SK, int ZS, bool Tiles = true>
 __global__ __launch_bounds__(kCkBlock) void chunk_post_pre_rows_kernel(const float* __restrict__ part, int splits, int M,
                                                                        const void* scale,
                                                                        const uint16_t* __restrict__ w_post,
@@ -770,7 +771,7 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_pre_rows_kernel(const flo
                                                                        uint16_t* __restrict__ hout) {
     __shared__ float red[4];
     __shared__ __attribute__((aligned(16))) uint16_t row[kH];
-    const int t = threadIdx.x, m = tile_row(blockIdx.x, gridDim.x);
+    const int t = threadIdx.x, m = Tiles ? tile_row(blockIdx.x, gridDim.x) : blockIdx.x;
     const int c = min(t, kH / 16 - 1);
     float wv[16];
     bf16x8_to_f32(ld16(w_pre + c * 16), wv);
@@ -784,7 +785,7 @@ __global__ __launch_bounds__(kCkBlock) void chunk_post_pre_rows_kernel(const flo
     float xv[16];
     bf16x8_to_f32(*reinterpret_cast<const uint4*>(row + c * 16), xv);
     bf16x8_to_f32(*reinterpret_cast<const uint4*>(row + c * 16 + 8), xv + 8);
-    rms_row_store<true>(xv, wv, m, red, hout);
+    rms_row_store<Tiles>(xv, wv, m, red, hout);
 }
 
 template <typename K, typename... A>
@@ -965,6 +966,16 @@ hipError_t launch_post_rows(const float* part, int splits, int M, const void* sc
                             uint16_t* res, const uint16_t* ls, hipStream_t s) {
     return sk == ScaleKind::F32 ? post_rows<ScaleKind::F32>(part, splits, M, scale, w_post, res, ls, s)
                                 : post_rows<ScaleKind::BF16>(part, splits, M, scale, w_post, res, ls, s);
+}
+
+hipError_t launch_post_pre_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk,
+                                const uint16_t* w_post, uint16_t* res, const uint16_t* w_pre, uint16_t* hout, hipStream_t s) {
+    if (splits > 4) return hipErrorInvalidValue;
+    return sk == ScaleKind::F32
+        ? ck_launch(chunk_post_pre_rows_kernel<ScaleKind::F32, 4, false>, dim3(M), s, part, splits, M, scale, w_post, res,
+                    w_pre, hout)
+        : ck_launch(chunk_post_pre_rows_kernel<ScaleKind::BF16, 4, false>, dim3(M), s, part, splits, M, scale, w_post, res,
+                    w_pre, hout);
 }
 
 hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, hipStream_t s) {

@@ -25,10 +25,6 @@ namespace moa {
 namespace {
 
 constexpr int kBlock = 256;  // four waves
-// Calls of at least this many rows (and at most kMaxDecodeM) run QKV and O, sliding and full, on
-// the matrix-core rows path (moa_rows.hip), which reads the weights once instead of once per row
-// (full-attention O from two rows). At two rows the per-row kernels are as fast.
-constexpr int kRowsProjMinM = 3;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }

@@ -10,6 +10,10 @@ namespace moa {
 
 // Rows handled by the decode (GEMV) kernels in one launch; larger M goes to the MFMA path.
 constexpr int kMaxDecodeM = 16;
+// Calls of at least this many rows (and at most kMaxDecodeM) run QKV and O, sliding and full, on
+// the matrix-core rows path (moa_rows.hip), which reads the weights once instead of once per row
+// (full-attention O from two rows). At two rows the per-row kernels are as fast.
+constexpr int kRowsProjMinM = 3;
 // Rows handled by one call of the MFMA (M > kMaxDecodeM) path; larger calls are tiled by the host.
 constexpr int kMaxChunkM = 1024;
 // QKV projection rows (Q | K | V).
@@ -180,10 +184,17 @@ hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* o
 hipError_t launch_qkv_heads(const QkvParams& p, int m0, int M, const float* part, int splits, hipStream_t s, DevCtx* ctx);
 hipError_t launch_post_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk, const uint16_t* w_post,
                             uint16_t* res, const uint16_t* ls, hipStream_t s);
+// The O post rows with the FFN's pre-norm behind them (splits <= 4): the new residual rows into res,
+// and bf16(RMSNorm(new residual) * w_pre) row-major into hout [M][kH].
+hipError_t launch_post_pre_rows(const float* part, int splits, int M, const void* scale, ScaleKind sk,
+                                const uint16_t* w_post, uint16_t* res, const uint16_t* w_pre, uint16_t* hout, hipStream_t s);
 // sliding_project_qkv and sliding / full attention output for 2..kMaxDecodeM rows on the matrix cores
 // (moa_rows.hip).
 hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
+// sliding_attention_output then decoder_feedforward on one residual for 2..kMaxDecodeM rows: O's post
+// rows also write the FFN's normalised input, so the FFN starts at its up/gate contraction.
+hipError_t launch_o_ffn_rows(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_full_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 
 // ops::final_norm_and_logits for M token rows (input [M][kH], out [M][kW]).

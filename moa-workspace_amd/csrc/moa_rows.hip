@@ -370,9 +370,10 @@ hipError_t rw_launch(dim3 grid, hipStream_t s, const FfnParams& p, const uint16_
     return hipGetLastError();
 }
 
+// normed: the pre-norm's rows are already in ctx->hbuf (launch_o_ffn_rows)
 template <FfnFormat F, ScaleKind SK>
-hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
-    hipError_t e = launch_rmsnorm_rows(p.residual + (size_t)m0 * kH, p.pre_rms, ctx->hbuf, M, s);
+hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed = false) {
+    hipError_t e = normed ? hipSuccess : launch_rmsnorm_rows(p.residual + (size_t)m0 * kH, p.pre_rms, ctx->hbuf, M, s);
     if (e != hipSuccess) return e;
     e = rw_launch<F, SK, true>(dim3(kRwUpGroups, 1, 1), s, p, ctx->hbuf, kH, M, ctx->pbuf, nullptr);
     if (e != hipSuccess) return e;
@@ -550,16 +551,37 @@ hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx*
                             p.residual + (size_t)m0 * kH, nullptr, s);
 }
 
-hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
-    if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
+static hipError_t ffn_rows_dispatch(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed) {
     switch (p.fmt) {
         case FfnFormat::FP8:
-            return p.scale_kind == ScaleKind::F32 ? rows_ffn_impl<FfnFormat::FP8, ScaleKind::F32>(p, m0, M, s, ctx)
-                                                  : rows_ffn_impl<FfnFormat::FP8, ScaleKind::BF16>(p, m0, M, s, ctx);
-        case FfnFormat::NVFP4: return rows_ffn_impl<FfnFormat::NVFP4, ScaleKind::F32>(p, m0, M, s, ctx);
-        case FfnFormat::MXFP4: return rows_ffn_impl<FfnFormat::MXFP4, ScaleKind::F32>(p, m0, M, s, ctx);
+            return p.scale_kind == ScaleKind::F32 ? rows_ffn_impl<FfnFormat::FP8, ScaleKind::F32>(p, m0, M, s, ctx, normed)
+                                                  : rows_ffn_impl<FfnFormat::FP8, ScaleKind::BF16>(p, m0, M, s, ctx, normed);
+        case FfnFormat::NVFP4: return rows_ffn_impl<FfnFormat::NVFP4, ScaleKind::F32>(p, m0, M, s, ctx, normed);
+        case FfnFormat::MXFP4: return rows_ffn_impl<FfnFormat::MXFP4, ScaleKind::F32>(p, m0, M, s, ctx, normed);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    if (M < 1 || M > kMaxDecodeM) return hipErrorInvalidValue;
+    return ffn_rows_dispatch(p, m0, M, s, ctx, false);
+}
+
+// O's contraction as launch_o_rows runs it, then one row kernel for O's post rows and the FFN's
+// pre-norm (the bits of chunk_post_rows_kernel, then of chunk_rmsnorm_rows_kernel<false>), then the
+// FFN's rows path from its up/gate contraction on.
+hipError_t launch_o_ffn_rows(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    if (M < 1 || M > kMaxDecodeM || o.div || o.residual != p.residual) return hipErrorInvalidValue;
+    ProjRows a{};
+    a.x = o.x + (size_t)m0 * kQs; a.M = M; a.K = kQs; a.N = kH;
+    a.w[0] = o.ow; a.nseg[0] = 0; a.nseg[1] = kH; a.nsegs = 1;
+    a.yf = ctx->fbuf;
+    hipError_t e = rw_proj<kRwOKR>(a, s);
+    if (e != hipSuccess) return e;
+    e = launch_post_pre_rows(ctx->fbuf, kQs / kRwOKR, M, o.os, o.scale_kind, o.post_rms, o.residual + (size_t)m0 * kH,
+                             p.pre_rms, ctx->hbuf, s);
+    if (e != hipSuccess) return e;
+    return ffn_rows_dispatch(p, m0, M, s, ctx, true);
 }
 
 }  // namespace moa

@@ -2,11 +2,12 @@
 FO/src/host/runtime.rs:440-459 then 543-571) on the GPU. The residual afterwards must have the same
 bits as sliding_attention_output followed by decoder_feedforward through their own entry points,
 and meet the gate against the oracle's chain of the two operators; one token row runs as one
-launch (o_ffn_fused_kernel), several rows as the two operators in turn."""
+launch (o_ffn_fused_kernel); from three rows on O's post rows also write the FFN's normalised
+input (one kernel fewer), and two rows run the two operators in turn."""
 import numpy as np
 import pytest
 
-from gpu_util import dev, gate, host, need_gpu, say
+from gpu_util import dev, gate, gate_addend, host, need_gpu, say
 from kat_inputs import ffn_stress_inputs, unbf
 from moa_amd import prng, synth
 from oracle import oracle as O
@@ -137,11 +138,46 @@ def test_zero_attention_row_then_ffn_stress_known_answer():
     assert np.all(got == 0x3ECF), np.unique(got)
 
 
-def test_rows_run_the_two_operators():
-    """Three token rows: the entry point runs the operators in turn (the same bits as the two calls)."""
+def test_two_rows_run_the_two_operators():
+    """Two token rows: the entry point runs the operators in turn (the same bits as the two calls)."""
     need_gpu()
-    say("o->ffn fp8 M3")
-    check("fp8", synth.cfg_o(0, M=3), synth.cfg_ffn_fp8(0, M=3), "o->ffn fp8 M3")
+    say("o->ffn fp8 M2")
+    check("fp8", synth.cfg_o(0, M=2), synth.cfg_ffn_fp8(0, M=2), "o->ffn fp8 M2")
+
+
+# 3..16 rows: the rows path, where O's post rows write the FFN's row-major normalised input
+# (chunk_post_pre_rows_kernel<.., false>) and the FFN starts at its up/gate contraction
+@pytest.mark.parametrize("fmt,M", [("fp8", 3), ("fp8", 7), ("fp8", 16), ("mxfp4", 16), ("nvfp4", 5)])
+def test_rows_path_writes_the_ffn_input_with_the_o_post_norm(fmt, M):
+    need_gpu()
+    say(f"o->ffn {fmt} M{M} (rows path)")
+    o, f = chunk_inputs(fmt, M)
+    check(fmt, o, f, f"o->ffn {fmt} M{M} rows")
+
+
+def test_rows_path_without_post_norm_and_scalar():
+    """Without the FFN's post-norm (a mode the reference operator does not have) d is added to the
+    residual unnormalised: the same bits as the two calls, and the oracle's chain within the gate
+    for such sums (gate_addend: an f32 sum in the matrix cores' order may round d one bf16 ulp
+    away from the oracle's, and that step reaches the output where r + d cancels)."""
+    need_gpu()
+    say("o->ffn fp8 M4 (rows path) without post-norm and layer scalar")
+    o, f = chunk_inputs("fp8", 4)
+    got = gpu_fused("fp8", o, f, False, False)
+    two = gpu_two_calls("fp8", o, f, False, False)
+    assert np.array_equal(got, two), f"{np.count_nonzero(got != two)} elements differ from the two calls"
+    mid = o["residual"].copy()
+    O.sliding_attention_output(o["x"], o["post_attn_rms_weight"], o["o_weight"], o_scale(o, False), mid)
+    gate_addend(oracle_chain("fp8", o, f, False, False), got, mid, "o->ffn fp8 M4 rows literal", atol=FFN_ATOL)
+
+
+def test_rows_path_bf16_o_scales():
+    """The bf16-scale O entry point's rows path (the NVFP4 entry point takes bf16 O scales)
+    feeding the FFN: O's scales read as bf16 by the shared row kernel."""
+    need_gpu()
+    say("o->ffn nvfp4 M16 (rows path, bf16 O scales)")
+    o, f = chunk_inputs("nvfp4", 16)
+    check("nvfp4", o, f, "o->ffn nvfp4 M16 rows")
 
 
 def test_interleaved_with_the_ffn_entry_point():
