@@ -1398,6 +1398,10 @@ constexpr int kFfnWgRows = kH / kFfnGrid;           // 16 down rows per workgrou
 constexpr int kFfnCtl = kFfnWaves - 1;              // the control wave
 constexpr int kFfnDownR = kFfnWgRows / kFfnWaves;   // 2 down rows per wave
 constexpr int kFfnDownPre = 8;                      // down chunks per row loaded before p is staged (FP8; 6-10 measured alike, 12 spills)
+// FP8 down chunks per row loaded right behind the reads of p (ffn_fused_kernel; graph-replayed
+// 30.60 -> 30.29 us with 3, 30.46 with 2, 30.51 with 4). FP4 rows load none there (1 or 2 measured
+// alike or slower), nor does o_ffn_fused_kernel (3: no change).
+constexpr int kFfnDownPost = 3;
 constexpr int kFfnDownPreFp4 = 4;                   // the same for FP4 rows (8 chunks; measured: 2 equal, 6 and 8 slower)
 static_assert(kFfnGrid == kFfnEpochCounters * kFfnEpochPer, "equal workgroups per epoch counter");
 static_assert(kFfnDownR * kFfnWaves == kFfnWgRows, "two down rows per wave");
@@ -1431,7 +1435,8 @@ struct FfnShared {
 // returned (control wave, lane 0); dscale: down scale of row drow0 + lane (lanes < kFfnDownR);
 // control wave: r8 / w8 a leader's residual and post-norm weight values at post_leader_row (with
 // the post-norm), r1 the residual value of row 16 b + lane (without it), ls_bits the layer scalar.
-template <FfnFormat F, ScaleKind SK>
+// LS: down chunks per row issued right behind the first reads of p.
+template <FfnFormat F, ScaleKind SK, int LS = 0>
 __device__ __forceinline__ void ffn_down_post(const FfnParams& p, const FfnShared& s, float pv, uint32_t ep_tag,
                                               uint32_t claim_old, uint16_t* res, int drow0, float dscale,
                                               const uint4& r8, const uint4& w8, uint32_t r1, uint32_t ls_bits,
@@ -1463,7 +1468,12 @@ __device__ __forceinline__ void ffn_down_post(const FfnParams& p, const FfnShare
     // would queue ahead of the slower waves' up/gate loads, which the barrier waits for).
     constexpr int PDW = F == FfnFormat::FP8 ? kFfnDownPre : kFfnDownPreFp4;
     constexpr int PD = PDW < KD ? PDW : KD;
-    constexpr int RS = PD < KD ? PD + 1 : KD;  // ring slots
+    // Chunks [0, PD) of the wave's rows are loaded ahead of the reads of p, chunks [PD, PR) right
+    // behind them (so that the memory keeps streaming while p comes back), the rest through the
+    // ring while the dots run.
+    constexpr int PA = PD + LS <= KD ? LS : KD - PD;
+    constexpr int PR = PD + PA;
+    constexpr int RS = PR < KD ? PR + 1 : PR;  // ring slots
     Chunk<F> ring[RS][kFfnDownR];
     {
         // p by tagged words instead of a barrier. The control wave's 32 words (two GeGLU values and
@@ -1490,29 +1500,52 @@ __device__ __forceinline__ void ffn_down_post(const FfnParams& p, const FfnShare
         uint64_t pw[PW];
 #pragma unroll
         for (int i = 0; i < PW; ++i) pw[i] = collect64(ptag + pword(i));
+        if constexpr (PA > 0) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = PD; j < PR; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const uint64_t t0 = wall_clock64();
         bool stalled = false;
-        for (;;) {
+        auto current = [&]() {
             bool ok = true;
 #pragma unroll
             for (int i = 0; i < PW; ++i) ok = ok && (uint32_t)(pw[i] >> 32) == tag;
-            if (__all(ok)) break;
+            return __all(ok) != 0;
+        };
+        // One round of the wait: false while the words are still stale and time is left.
+        auto poll = [&]() {
             const uint64_t dt = wall_clock64() - t0;
             if (dt > kSpinTicks) {
                 if (lane == 0) {
                     atomicOr(err, kErrSpinTimeout);
                     s_expired = 1u;
                 }
-                break;
+                return true;
             }
             if (__builtin_expect(dt > stall.steal_ticks, 0)) {
                 stalled = true;
                 if (lane == 0) s_stall = 1u;
-                break;
+                return true;
             }
             __builtin_amdgcn_s_sleep(1);
             // reload the words still carrying an older tag (unrolled at compile time)
             reload_stale(pw, tag, [&](int i) { return ptag + pword(i); }, std::make_integer_sequence<int, PW>{});
+            return current();
+        };
+        if constexpr (PA > 0) {
+            // The first check in straight-line code: the compiler then waits for the reads of p
+            // alone, not for the chunks behind them (at a loop head it waits for every load).
+            if (!current()) {
+                while (!poll()) {
+                }
+                // every load of this path complete, so that the compiler's count stays exact below
+                __builtin_amdgcn_s_waitcnt(0);
+            }
+        } else {
+            while (!current() && !poll()) {
+            }
         }
         if (!stalled) {
 #pragma unroll
@@ -1580,7 +1613,7 @@ __device__ __forceinline__ void ffn_down_post(const FfnParams& p, const FfnShare
             // The down prefetch again: the take-over used its registers (and with them, its
             // values are not kept live through the take-over).
 #pragma unroll
-            for (int j = 0; j < PD; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
+            for (int j = 0; j < PR; ++j) down_chunk_issue<F, kFfnDownR>(ring[j], p, drow0, kFfnDownR, j, lane);
             __syncthreads();  // p staged
         }
     }
@@ -1592,7 +1625,7 @@ __device__ __forceinline__ void ffn_down_post(const FfnParams& p, const FfnShare
         for (int r = 0; r < kFfnDownR; ++r) acc[r] = 0.0f;
 #pragma unroll
         for (int j = 0; j < KD; ++j) {
-            if (j + PD < KD) down_chunk_issue<F, kFfnDownR>(ring[(j + PD) % RS], p, drow0, kFfnDownR, j + PD, lane);
+            if (j + PR < KD) down_chunk_issue<F, kFfnDownR>(ring[(j + PR) % RS], p, drow0, kFfnDownR, j + PR, lane);
             const int e0 = j * 64 * EPC + lane * EPC;
             if (e0 < kL) {
                 uint32_t x[EPC / 2];
@@ -1677,6 +1710,7 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
     __shared__ float red[kFfnWaves];
     __shared__ float pl[kFfnWaves * kUgRL];
     __shared__ uint32_t dl[kFfnWgRows];
+    constexpr int kLs = F == FfnFormat::FP8 ? kFfnDownPost : 0;
     __shared__ uint32_t s_tag, s_expired, s_stall;
     __shared__ int s_victim;
     const FfnShared s{sh, sx, red, pl, dl, &s_tag, &s_expired, &s_stall, &s_victim};
@@ -1724,7 +1758,7 @@ void ffn_fused_kernel(FfnParams p, int m0, uint64_t* ptag, PostSlots* slots, uin
     };
     const int lbase = blockIdx.x * (kFfnWaves * kUgRL) + wave;
     const float pv = up_gate_rows<F, SK, kFfnWaves>(p, res, lbase, kFfnWaves, sh, red, claim);
-    ffn_down_post<F, SK>(p, s, pv, ep_tag, claim_old, res, drow0, dscale, r8, w8, r1, ls_bits, ptag, slots, err,
+    ffn_down_post<F, SK, kLs>(p, s, pv, ep_tag, claim_old, res, drow0, dscale, r8, w8, r1, ls_bits, ptag, slots, err,
                          stall);
 }
 
