@@ -64,6 +64,9 @@ BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          # config 3, MXFP4 weights (E2M1 codes + E8M0 block-32 scales) at M = 1 and M = 16 rows: the
          # weights once, plus the rows' residual read and write, the two norm weights, the layer scalar
          "ffn_mxfp4": 94_003_200 + 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
+         # the reference's own FFN operand types (NVFP4: E2M1 codes, E4M3 block-16 scales, three f32
+         # reciprocal global scales) on its run-0 inputs, M = 1
+         "ffn_nvfp4": 3 * 29_491_200 + 3 * 3_686_400 + 3 * 4 + 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
          "ffn_mxfp4_m16": 94_003_200 + 16 * 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
          # O at 16 rows (15 more input rows and residual rows read and written), and O then the
          # MXFP4 FFN on those 16 residual rows through one entry point (less the rows between them)
@@ -110,7 +113,7 @@ def main() -> int:
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
-                                          "ffn_mxfp4", "ffn_mxfp4_m16", "o_ffn", "o_m16", "o_ffn_mxfp4_m16",
+                                          "ffn_mxfp4", "ffn_mxfp4_m16", "ffn_nvfp4", "o_ffn", "o_m16", "o_ffn_mxfp4_m16",
                                           "chunk", "chunk_o_ffn", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
@@ -202,6 +205,13 @@ def main() -> int:
     MXW = replicate(mx, MXK, nmx)
     mx_res16 = dev(mx["residual"])
     mx_res1 = mx_res16[:1].clone()
+    nv = synth.ref_ffn_inputs(0)
+    NVK = ("up_weight_packed", "gate_weight_packed", "down_weight_packed", "up_weight_scale", "gate_weight_scale",
+           "down_weight_scale", "up_global_scale", "gate_global_scale", "down_global_scale")
+    nnv = copies(BYTES["ffn_nvfp4"])
+    NVW = replicate(nv, NVK, nnv)
+    nv_res, nv_pre, nv_post, nv_ls = (dev(nv[k]) for k in ("residual", "pre_ff_rms_weight", "post_ff_rms_weight",
+                                                             "layer_scalar"))
     o_x16 = dev(synth.bf16_normal("bench.o.x16", (16, 4096)))  # 16 attention rows for O at M = 16
     o_x, o_post, o_res = dev(o["x"]), dev(o["post_attn_rms_weight"]), dev(o["residual"])
     q = {k: dev(qkv[k]) for k in ("x", "input_rms_weight", "q_rms_weight", "k_rms_weight", "cos", "sin",
@@ -270,6 +280,10 @@ def main() -> int:
     def run_ffn_mxfp4(i, res=None):
         w = MXW[i % nmx]
         ops.decoder_feedforward_mxfp4(mx_res1 if res is None else res, f_pre, *[w[k] for k in MXK], f_post, f_ls)
+
+    def run_ffn_nvfp4(i):
+        w = NVW[i % nnv]
+        ops.decoder_feedforward(nv_res, nv_pre, *[w[k] for k in NVK], nv_post, nv_ls)
 
     def run_ffn_mxfp4_m16(i):
         run_ffn_mxfp4(i, mx_res16)
@@ -407,7 +421,8 @@ def main() -> int:
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
               "fattn_fused64": run_fattn_fused64, "fo": run_fo, "ffn_mxfp4": run_ffn_mxfp4,
               "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "chunk": run_layer, "chunk_o_ffn": run_layer_o_ffn,
-              "o_ffn": run_o_ffn, "o_m16": run_o_m16, "o_ffn_mxfp4_m16": run_o_ffn_mxfp4_m16}[args.profile]
+              "o_ffn": run_o_ffn, "o_m16": run_o_m16, "o_ffn_mxfp4_m16": run_o_ffn_mxfp4_m16,
+              "ffn_nvfp4": run_ffn_nvfp4}[args.profile]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
@@ -423,7 +438,8 @@ def main() -> int:
 
     per_op = {}
     for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("o_ffn", run_o_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
-                     ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("o_m16", run_o_m16), ("o_ffn_mxfp4_m16", run_o_ffn_mxfp4_m16),
+                     ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("ffn_nvfp4", run_ffn_nvfp4), ("o_m16", run_o_m16),
+                     ("o_ffn_mxfp4_m16", run_o_ffn_mxfp4_m16),
                      ("attn", run_attn), ("logits", run_logits),
                      ("fqkv", run_fqkv), ("fattn", run_fattn), ("fattn_fused", run_fattn_fused),
                      ("fattn_fused64", run_fattn_fused64), ("fo", run_fo)):
