@@ -11,11 +11,13 @@
 // atol + rtol |expected|. Two changes, both stricter: atol is BASELINE's 1e-2 for all three
 // operators (the reference's table has 0.04 / 0.05 / 0.01), and a non-zero output whose sign
 // differs from an expected value of magnitude >= atol fails (BASELINE's sign-cancellation rule).
-// The QKV test also checks that every cache slot but the written one keeps its bits.
+// The QKV test also checks that every cache slot but the written one keeps its bits, and a last
+// check that the host interface rejects tensors of the wrong shape.
 //
 //   test_kernels [--runs N]      run on device 0 (N <= 9, default 3, the reference's RUNS)
 //   test_kernels --checksums     no GPU: print the checksum of every synthesised input
 //   test_kernels --list          print the test table
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -283,6 +285,28 @@ struct FfnCase {
     }
 };
 
+// The host interface rejects a call whose tensors do not have the operator's shapes, before
+// anything is launched (the reference's shapes are types, so there the call would not compile).
+bool rejects_bad_shapes(const Device& d) {
+    OCase c(0);
+    auto r = HbmTensor<bf16>::from_host(d, std::vector<bf16>(c.residual.begin(), c.residual.end() - 8), {moa::kH - 8});
+    const auto dx = hbm(d, c.x), dpost = hbm(d, c.post), dos = hbm(d, c.os);
+    const auto dow = hbm(d, c.ow);
+    int code = 0;
+    try {
+        moa::ops::sliding_attention_output(d, dx, dpost, dow, dos, r);
+    } catch (const moa::Error& e) {
+        code = e.code();
+    }
+    const auto after = r.to_host(d);
+    const bool untouched = std::equal(after.begin(), after.end(), c.residual.begin(),
+                                      [](bf16 a, bf16 b) { return a.bits == b.bits; });
+    const bool ok = code == MOA_ERROR_INVALID_VALUE && untouched;
+    std::printf("[%-40s] moa::Error code %d, residual %s -> %s\n", "host interface: a residual of 3832", code,
+                untouched ? "untouched" : "CHANGED", ok ? "PASS" : "FAIL");
+    return ok;
+}
+
 template <class Case>
 void print_checks(int run) {
     Case c(run);
@@ -335,12 +359,13 @@ int main(int argc, char** argv) {
                 failed += ok ? 0 : 1;
             }
         }
+        failed += rejects_bad_shapes(device) ? 0 : 1;
         const uint32_t bits = device.device_errors();
         if (bits) {
             std::printf("device error bits 0x%x -> FAIL\n", bits);
             ++failed;
         }
-        std::printf("%s: %d of %d checks failed\n", failed ? "FAIL" : "PASS", failed, 3 * runs + 1);
+        std::printf("%s: %d of %d checks failed\n", failed ? "FAIL" : "PASS", failed, 3 * runs + 2);
         return failed ? 1 : 0;
     } catch (const moa::Error& e) {
         std::printf("FAIL: %s (code %d)\n", e.what(), e.code());

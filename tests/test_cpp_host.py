@@ -62,5 +62,16 @@ def test_harness_passes_on_the_gpu():
     print(res.stdout, flush=True)
     assert res.returncode == 0, res.stdout + res.stderr
     lines = res.stdout.splitlines()
-    assert sum(1 for l in lines if l.rstrip().endswith("-> PASS")) == 3 * (4 + 1 + 1)
-    assert lines[-1].startswith("PASS: 0 of 10 checks failed")
+    assert sum(1 for l in lines if l.rstrip().endswith("-> PASS")) == 3 * (4 + 1 + 1) + 1
+    assert lines[-1].startswith("PASS: 0 of 11 checks failed")
+
+
+def test_harness_without_a_device_fails_with_the_library_error():
+    """No GPU (this container): moa::Device's set-up throws moa::Error carrying the library's
+    reason, and the harness exits 1 instead of aborting."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a device is visible")
+    res = run("--runs", "1")
+    assert res.returncode == 1, res.stdout + res.stderr
+    assert "FAIL:" in res.stdout and "code" in res.stdout, res.stdout
