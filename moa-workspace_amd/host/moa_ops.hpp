@@ -104,7 +104,9 @@ class Device {
     hipStream_t stream_ = nullptr;
 };
 
-// A device buffer of T with a shape, owned (hipMalloc'd at construction, freed at destruction).
+// A device buffer of T with a shape, owned: hipMalloc'd at construction, hipFree'd at destruction
+// (hipFree waits for the device's outstanding work, so a tensor may go out of scope right after an
+// operator that uses it).
 template <class T>
 class HbmTensor {
     static_assert(std::is_trivially_copyable<T>::value, "device tensors hold plain values");
