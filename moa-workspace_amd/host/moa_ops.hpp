@@ -118,8 +118,13 @@ class HbmTensor {
         n_ = std::accumulate(shape_.begin(), shape_.end(), size_t{1}, [](size_t a, size_t b) { return a * b; });
         d.make_current();
         check_hip(hipMalloc(reinterpret_cast<void**>(&ptr_), bytes()), "hipMalloc");
-        check_hip(hipMemsetAsync(ptr_, 0, bytes(), d.stream()), "hipMemsetAsync");
-        check_hip(hipStreamSynchronize(d.stream()), "hipStreamSynchronize");
+        try {
+            check_hip(hipMemsetAsync(ptr_, 0, bytes(), d.stream()), "hipMemsetAsync");
+            check_hip(hipStreamSynchronize(d.stream()), "hipStreamSynchronize");
+        } catch (...) {  // no destructor runs for a constructor that throws
+            (void)hipFree(ptr_);
+            throw;
+        }
     }
     // The host values, uploaded (HostTensor::to_hbm).
     static HbmTensor from_host(const Device& d, const std::vector<T>& host, std::vector<size_t> shape) {
