@@ -15,6 +15,7 @@
 // check that the host interface rejects tensors of the wrong shape.
 //
 //   test_kernels [--runs N]      run on device 0 (N <= 9, default 3, the reference's RUNS)
+//   test_kernels --time CALLS    then time each operator host-driven through moa::ops
 //   test_kernels --checksums     no GPU: print the checksum of every synthesised input
 //   test_kernels --list          print the test table
 #include <algorithm>
@@ -307,6 +308,103 @@ bool rejects_bad_shapes(const Device& d) {
     return ok;
 }
 
+// ---------------------------------------------------------------- host-driven timing
+// Each operator on run 0's inputs, `calls` calls back to back from the host through moa::ops,
+// timed with HIP events on the device's stream (median of 5 batches). The weights rotate over
+// copies of at least 512 MiB in all, so no call reads them from the 256 MB MALL.
+template <class T>
+HbmTensor<T> clone(const Device& d, const HbmTensor<T>& t) {
+    HbmTensor<T> c(d, t.shape());
+    moa::check_hip(hipMemcpyAsync(c.data(), t.data(), t.bytes(), hipMemcpyDeviceToDevice, d.stream()), "hipMemcpyAsync");
+    return c;
+}
+
+size_t copies_for(size_t bytes) { return std::max<size_t>(2, (512ull << 20) / bytes + 1); }
+
+template <class F>
+double time_calls(const Device& d, int calls, F&& call) {
+    for (int i = 0; i < 10; ++i) call(i);
+    d.synchronize();
+    hipEvent_t a, b;
+    moa::check_hip(hipEventCreate(&a), "hipEventCreate");
+    moa::check_hip(hipEventCreate(&b), "hipEventCreate");
+    std::vector<double> per;
+    for (int batch = 0; batch < 5; ++batch) {
+        moa::check_hip(hipEventRecord(a, d.stream()), "hipEventRecord");
+        for (int i = 0; i < calls; ++i) call(i);
+        moa::check_hip(hipEventRecord(b, d.stream()), "hipEventRecord");
+        moa::check_hip(hipEventSynchronize(b), "hipEventSynchronize");
+        float ms = 0.0f;
+        moa::check_hip(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+        per.push_back(1e3 * ms / calls);
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    std::sort(per.begin(), per.end());
+    return per[per.size() / 2];
+}
+
+void time_ops(const Device& d, int calls) {
+    {
+        QkvCase c(0);
+        const auto dx = hbm(d, c.x), dqs = hbm(d, c.qs), dks = hbm(d, c.ks), dvs = hbm(d, c.vs), din = hbm(d, c.in_rms),
+                   dqr = hbm(d, c.q_rms), dkr = hbm(d, c.k_rms), dcos = hbm(d, c.cos), dsin = hbm(d, c.sin);
+        const auto kv = hbm(d, std::vector<int32_t>{c.kv_offset}), ro = hbm(d, std::vector<int32_t>{c.rope_offset});
+        HbmTensor<bf16> gk(d, {TS, NS, DS}), gv(d, {TS, NS, DS}), gq(d, {NS, 2, DS});
+        std::vector<HbmTensor<moa::f8e4m3>> w;
+        w.push_back(hbm(d, c.qw)); w.push_back(hbm(d, c.kw)); w.push_back(hbm(d, c.vw));
+        const size_t n = copies_for((QS + 2 * PS) * H);
+        for (size_t i = 1; i < n; ++i)
+            for (int j = 0; j < 3; ++j) w.push_back(clone(d, w[j]));
+        const double us = time_calls(d, calls, [&](int i) {
+            const size_t k = 3 * (i % n);
+            moa::ops::sliding_project_qkv(d, dx, w[k], w[k + 1], w[k + 2], dqs, dks, dvs, din, dqr, dkr, kv, ro, dcos,
+                                          dsin, gk, gv, gq);
+        });
+        std::printf("[time %-35s] %8.2f us per call (%d calls, %zu weight copies)\n", "sliding_project_qkv", us, calls, n);
+    }
+    {
+        OCase c(0);
+        auto r = hbm(d, c.residual);
+        const auto dx = hbm(d, c.x), dpost = hbm(d, c.post), dos = hbm(d, c.os);
+        std::vector<HbmTensor<moa::f8e4m3>> w;
+        w.push_back(hbm(d, c.ow));
+        const size_t n = copies_for(H * QS);
+        for (size_t i = 1; i < n; ++i) w.push_back(clone(d, w[0]));
+        const double us = time_calls(d, calls, [&](int i) {
+            moa::ops::sliding_attention_output(d, dx, dpost, w[i % n], dos, r);
+        });
+        std::printf("[time %-35s] %8.2f us per call (%d calls, %zu weight copies)\n", "sliding_attention_output", us, calls,
+                    n);
+    }
+    {
+        FfnCase c(0);
+        auto r = hbm(d, c.residual);
+        const auto dpre = hbm(d, c.pre), dpost = hbm(d, c.post), dls = hbm(d, c.ls);
+        const auto dgu = hbm(d, std::vector<float>{c.inv_g[0]}), dgg = hbm(d, std::vector<float>{c.inv_g[1]}),
+                   dgd = hbm(d, std::vector<float>{c.inv_g[2]});
+        std::vector<HbmTensor<moa::f4e2m1x2>> wp;
+        std::vector<HbmTensor<moa::f8e4m3>> ws;
+        for (int j = 0; j < 3; ++j) {
+            wp.push_back(hbm(d, c.packed[j]));
+            ws.push_back(hbm(d, c.scale[j]));
+        }
+        const size_t n = copies_for(3 * (L * H / 2 + L * H / 16));
+        for (size_t i = 1; i < n; ++i)
+            for (int j = 0; j < 3; ++j) {
+                wp.push_back(clone(d, wp[j]));
+                ws.push_back(clone(d, ws[j]));
+            }
+        const double us = time_calls(d, calls, [&](int i) {
+            const size_t k = 3 * (i % n);
+            moa::ops::decoder_feedforward(d, r, dpre, wp[k], wp[k + 1], wp[k + 2], ws[k], ws[k + 1], ws[k + 2], dgu, dgg,
+                                          dgd, dpost, dls);
+        });
+        std::printf("[time %-35s] %8.2f us per call (%d calls, %zu weight copies)\n", "decoder_feedforward (NVFP4)", us,
+                    calls, n);
+    }
+}
+
 template <class Case>
 void print_checks(int run) {
     Case c(run);
@@ -318,10 +416,17 @@ void print_checks(int run) {
 
 int main(int argc, char** argv) {
     int runs = 3;  // FO/src/bin/test_kernels.rs:168
+    int timed_calls = 0;
     bool checksums = false;
     for (int i = 1; i < argc; ++i) {
         if (!std::strcmp(argv[i], "--runs") && i + 1 < argc) {
             runs = std::atoi(argv[++i]);
+        } else if (!std::strcmp(argv[i], "--time") && i + 1 < argc) {
+            timed_calls = std::atoi(argv[++i]);
+            if (timed_calls < 1 || timed_calls > 100000) {
+                std::fprintf(stderr, "--time takes 1..100000 calls\n");
+                return 2;
+            }
         } else if (!std::strcmp(argv[i], "--checksums")) {
             checksums = true;
         } else if (!std::strcmp(argv[i], "--list")) {
@@ -330,7 +435,7 @@ int main(int argc, char** argv) {
                             kAtol, kRtol);
             return 0;
         } else {
-            std::fprintf(stderr, "usage: %s [--runs N] [--checksums] [--list]\n", argv[0]);
+            std::fprintf(stderr, "usage: %s [--runs N] [--time CALLS] [--checksums] [--list]\n", argv[0]);
             return 2;
         }
     }
@@ -366,6 +471,7 @@ int main(int argc, char** argv) {
             ++failed;
         }
         std::printf("%s: %d of %d checks failed\n", failed ? "FAIL" : "PASS", failed, 3 * runs + 2);
+        if (!failed && timed_calls) time_ops(device, timed_calls);
         return failed ? 1 : 0;
     } catch (const moa::Error& e) {
         std::printf("FAIL: %s (code %d)\n", e.what(), e.code());
