@@ -16,6 +16,8 @@
 //
 //   test_kernels [--runs N]      run on device 0 (N <= 9, default 3, the reference's RUNS)
 //   test_kernels --time CALLS    then time each operator host-driven through moa::ops
+//   test_kernels --graph         then capture a decode step into a HIP graph; its replays must
+//                                leave the eager step's bits
 //   test_kernels --checksums     no GPU: print the checksum of every synthesised input
 //   test_kernels --list          print the test table
 #include <algorithm>
@@ -405,6 +407,79 @@ void time_ops(const Device& d, int calls) {
     }
 }
 
+// ---------------------------------------------------------------- HIP graph
+// The runtime's sliding-layer step without its attention (FO/src/host/runtime.rs:411-459,
+// 543-571) on run 0's inputs: QKV, then O and the FFN on one residual, captured from the device's
+// stream into a HIP graph through moa::ops. Each replay must leave the bits of the same calls made
+// eagerly (the state is restored from copies before each step, inside the graph), with eager work
+// and synchronisations between the replays.
+bool graph_step(const Device& d) {
+    QkvCase q(0);
+    OCase o(0);
+    FfnCase f(0);
+    const auto kv = hbm(d, std::vector<int32_t>{q.kv_offset}), ro = hbm(d, std::vector<int32_t>{q.rope_offset});
+    const auto qx = hbm(d, q.x), qqs = hbm(d, q.qs), qks = hbm(d, q.ks), qvs = hbm(d, q.vs), qin = hbm(d, q.in_rms),
+               qqr = hbm(d, q.q_rms), qkr = hbm(d, q.k_rms), qcos = hbm(d, q.cos), qsin = hbm(d, q.sin);
+    const auto qqw = hbm(d, q.qw), qkw = hbm(d, q.kw), qvw = hbm(d, q.vw);
+    const auto ox = hbm(d, o.x), opost = hbm(d, o.post), oos = hbm(d, o.os);
+    const auto oow = hbm(d, o.ow);
+    const auto fpre = hbm(d, f.pre), fpost = hbm(d, f.post), fls = hbm(d, f.ls);
+    const auto fup = hbm(d, f.packed[0]), fgate = hbm(d, f.packed[1]), fdown = hbm(d, f.packed[2]);
+    const auto fsu = hbm(d, f.scale[0]), fsg = hbm(d, f.scale[1]), fsd = hbm(d, f.scale[2]);
+    const auto fgu = hbm(d, std::vector<float>{f.inv_g[0]}), fgg = hbm(d, std::vector<float>{f.inv_g[1]}),
+               fgd = hbm(d, std::vector<float>{f.inv_g[2]});
+    const auto res0 = hbm(d, o.residual);
+    HbmTensor<bf16> res(d, {H}), kc(d, {TS, NS, DS}), vc(d, {TS, NS, DS}), qo(d, {NS, 2, DS});
+    const HbmTensor<bf16> zero_cache(d, {TS, NS, DS});
+    auto copy = [&](HbmTensor<bf16>& dst, const HbmTensor<bf16>& src) {
+        moa::check_hip(hipMemcpyAsync(dst.data(), src.data(), src.bytes(), hipMemcpyDeviceToDevice, d.stream()),
+                       "hipMemcpyAsync");
+    };
+    auto step = [&] {
+        copy(res, res0);
+        copy(kc, zero_cache);
+        copy(vc, zero_cache);
+        moa::ops::sliding_project_qkv(d, qx, qqw, qkw, qvw, qqs, qks, qvs, qin, qqr, qkr, kv, ro, qcos, qsin, kc, vc, qo);
+        moa::ops::sliding_attention_output(d, ox, opost, oow, oos, res);
+        moa::ops::decoder_feedforward(d, res, fpre, fup, fgate, fdown, fsu, fsg, fsd, fgu, fgg, fgd, fpost, fls);
+    };
+    auto snapshot = [&] {
+        auto a = res.to_host(d), b = qo.to_host(d), c = kc.to_host(d), e = vc.to_host(d);
+        a.insert(a.end(), b.begin(), b.end());
+        a.insert(a.end(), c.begin(), c.end());
+        a.insert(a.end(), e.begin(), e.end());
+        return a;
+    };
+    step();
+    const auto want = snapshot();
+
+    auto capture = [&](int n) {
+        hipGraph_t g;
+        hipGraphExec_t x;
+        moa::check_hip(hipStreamBeginCapture(d.stream(), hipStreamCaptureModeGlobal), "hipStreamBeginCapture");
+        for (int i = 0; i < n; ++i) step();
+        moa::check_hip(hipStreamEndCapture(d.stream(), &g), "hipStreamEndCapture");
+        moa::check_hip(hipGraphInstantiate(&x, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+        moa::check_hip(hipGraphDestroy(g), "hipGraphDestroy");
+        return x;
+    };
+    bool ok = true;
+    {
+        hipGraphExec_t one = capture(1);
+        for (int r = 0; r < 3 && ok; ++r) {
+            moa::check_hip(hipGraphLaunch(one, d.stream()), "hipGraphLaunch");
+            const auto got = snapshot();
+            ok = std::equal(got.begin(), got.end(), want.begin(), [](bf16 a, bf16 b) { return a.bits == b.bits; });
+            step();  // eager work between the replays
+            d.synchronize();
+        }
+        (void)hipGraphExecDestroy(one);
+    }
+    std::printf("[%-40s] 3 replays of the captured step vs the eager step: %s -> %s\n", "graph: QKV, O, FFN",
+                ok ? "same bits" : "DIFFER", ok ? "PASS" : "FAIL");
+    return ok;
+}
+
 template <class Case>
 void print_checks(int run) {
     Case c(run);
@@ -417,6 +492,7 @@ void print_checks(int run) {
 int main(int argc, char** argv) {
     int runs = 3;  // FO/src/bin/test_kernels.rs:168
     int timed_calls = 0;
+    bool graph = false;
     bool checksums = false;
     for (int i = 1; i < argc; ++i) {
         if (!std::strcmp(argv[i], "--runs") && i + 1 < argc) {
@@ -427,6 +503,8 @@ int main(int argc, char** argv) {
                 std::fprintf(stderr, "--time takes 1..100000 calls\n");
                 return 2;
             }
+        } else if (!std::strcmp(argv[i], "--graph")) {
+            graph = true;
         } else if (!std::strcmp(argv[i], "--checksums")) {
             checksums = true;
         } else if (!std::strcmp(argv[i], "--list")) {
@@ -435,7 +513,7 @@ int main(int argc, char** argv) {
                             kAtol, kRtol);
             return 0;
         } else {
-            std::fprintf(stderr, "usage: %s [--runs N] [--time CALLS] [--checksums] [--list]\n", argv[0]);
+            std::fprintf(stderr, "usage: %s [--runs N] [--time CALLS] [--graph] [--checksums] [--list]\n", argv[0]);
             return 2;
         }
     }
@@ -472,6 +550,7 @@ int main(int argc, char** argv) {
         }
         std::printf("%s: %d of %d checks failed\n", failed ? "FAIL" : "PASS", failed, 3 * runs + 2);
         if (!failed && timed_calls) time_ops(device, timed_calls);
+        if (!failed && graph && !graph_step(device)) failed = 1;
         return failed ? 1 : 0;
     } catch (const moa::Error& e) {
         std::printf("FAIL: %s (code %d)\n", e.what(), e.code());

@@ -58,16 +58,18 @@ def test_harness_passes_on_the_gpu():
     from gpu_util import need_gpu, say
     need_gpu()
     say("C++ harness, runs 0-2")
-    res = run("--runs", "3", "--time", "50", timeout=300)
+    res = run("--runs", "3", "--time", "50", "--graph", timeout=300)
     print(res.stdout, flush=True)
     assert res.returncode == 0, res.stdout + res.stderr
     lines = res.stdout.splitlines()
-    assert sum(1 for l in lines if l.rstrip().endswith("-> PASS")) == 3 * (4 + 1 + 1) + 1
+    assert sum(1 for l in lines if l.rstrip().endswith("-> PASS")) == 3 * (4 + 1 + 1) + 1 + 1
     assert any(l.startswith("PASS: 0 of 11 checks failed") for l in lines)
     # host-driven through moa::ops: one line per operator, a positive time per call
     times = [l for l in lines if l.startswith("[time ")]
     assert len(times) == 3
     assert all(float(l.split("]")[1].split()[0]) > 0 for l in times)
+    # the step captured into a HIP graph through moa::ops replays with the eager bits
+    assert any(l.startswith("[graph: QKV, O, FFN") and l.rstrip().endswith("-> PASS") for l in lines)
 
 
 def test_harness_without_a_device_fails_with_the_library_error():
