@@ -300,6 +300,12 @@ int moa_test_preset_epochs(uint64_t launches);
  * steal_ticks 0 restores the defaults (no hold). */
 int moa_test_set_stall(uint32_t steal_ticks, uint32_t hold_ticks, const int32_t* hold);
 
+/* Test support (no counterpart in the reference): with on == 0, later decoder_feedforward calls of
+ * 2..16 rows (and the rows path of sliding_attention_output_feedforward) run the up/gate and the
+ * down contractions as two launches instead of one, so that a test can compare the two (they give
+ * the same bits); on != 0 restores the default, one launch where its grid fits on the device. */
+int moa_test_set_rows_one_launch(int on);
+
 /* Test support: the number of take-overs (a wait that did another workgroup's share) on the
  * current device since the last call, in the scratch of every entry point that has run there
  * (the no-allocation entry point's included), then resets it. Synchronises the device. */

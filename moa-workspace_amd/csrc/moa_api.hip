@@ -87,6 +87,7 @@ DevCtx* device_context(hipError_t* err) {
     const size_t t_ofnpart = carve(sizeof(uint64_t) * kFfnSlotWords * kOfnCopies);
     const size_t t_qpart = carve(sizeof(uint64_t) * kQkvSlotWords);
     const size_t t_ptag = carve(sizeof(uint64_t) * (kL / 2));
+    const size_t t_rflag = carve(sizeof(uint64_t) * kRowsFlagWords);
     const size_t t_attn = carve(sizeof(float) * kAttnPartFloats);
     const size_t t_fattn = carve(sizeof(float) * kFattnPartFloats);
     int cus = 0;
@@ -115,6 +116,7 @@ DevCtx* device_context(hipError_t* err) {
     c.ofn_part = reinterpret_cast<uint64_t*>(b + t_ofnpart);
     c.qkv_part = reinterpret_cast<uint64_t*>(b + t_qpart);
     c.ffn_ptag = reinterpret_cast<uint64_t*>(b + t_ptag);
+    c.rows_flag = reinterpret_cast<uint64_t*>(b + t_rflag);
     c.attn_part = reinterpret_cast<float*>(b + t_attn);
     c.fattn_part = reinterpret_cast<float*>(b + t_fattn);
     c.base = base;
@@ -138,6 +140,7 @@ constexpr size_t kNaPtagBytes = sizeof(uint64_t) * (kL / 2);
 constexpr size_t kNaHBytes = sizeof(uint16_t) * kMaxDecodeM * kH;
 constexpr size_t kNaPBytes = sizeof(uint16_t) * kMaxDecodeM * kL;
 constexpr size_t kNaFBytes = sizeof(float) * 4 * kMaxDecodeM * kH;  // 4 down splits of the rows path
+constexpr size_t kNaRowsFlagBytes = sizeof(uint64_t) * kRowsFlagWords;
 constexpr size_t na_up(size_t v) { return (v + 255) / 256 * 256; }
 constexpr size_t kNaTicketOff = 0;
 constexpr size_t kNaErrOff = kNaTicketOff + na_up(kNaTicketBytes);
@@ -146,7 +149,8 @@ constexpr size_t kNaPtagOff = kNaPartOff + na_up(kNaPartBytes);
 constexpr size_t kNaHOff = kNaPtagOff + na_up(kNaPtagBytes);
 constexpr size_t kNaPOff = kNaHOff + na_up(kNaHBytes);
 constexpr size_t kNaFOff = kNaPOff + na_up(kNaPBytes);
-constexpr size_t kNaBytes = kNaFOff + na_up(kNaFBytes);  // 1.93 MB
+constexpr size_t kNaRowsFlagOff = kNaFOff + na_up(kNaFBytes);
+constexpr size_t kNaBytes = kNaRowsFlagOff + na_up(kNaRowsFlagBytes);  // 1.93 MB
 static_assert(kNaBytes < (2u << 20), "the no-allocation scratch stays under 2 MiB");
 
 static __device__ __align__(256) unsigned char scratch[kNaBytes];
@@ -184,6 +188,7 @@ DevCtx* noalloc_context(int* code) {
     c.hbuf = reinterpret_cast<uint16_t*>(b + kNaHOff);
     c.pbuf = reinterpret_cast<uint16_t*>(b + kNaPOff);
     c.fbuf = reinterpret_cast<float*>(b + kNaFOff);
+    c.rows_flag = reinterpret_cast<uint64_t*>(b + kNaRowsFlagOff);
     c.base = ptr;
     return &c;
 }
@@ -689,6 +694,11 @@ int moa_test_set_stall(uint32_t steal_ticks, uint32_t hold_ticks, const int32_t*
         for (int i = 0; i < 4 && hold; ++i) st.hold[i] = hold[i];
     }
     set_stall(st);
+    return MOA_SUCCESS;
+}
+
+int moa_test_set_rows_one_launch(int on) {
+    set_rows_one_launch(on != 0);
     return MOA_SUCCESS;
 }
 

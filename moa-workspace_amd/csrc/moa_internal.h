@@ -59,6 +59,9 @@ constexpr int kFfnPartSlots = 256;
 constexpr int kFfnSlotWords = kFfnPartSlots * 10;
 constexpr int kQkvSlotWords = 32 * 8;
 constexpr int kOfnCopies = 8;  // copies of O's post-norm words in the single-launch O -> FFN kernel
+// Tagged flags of the one-launch rows FFN (moa_rows.hip rows_fused_kernel): one per GeGLU block,
+// then one per block of down partial sums.
+constexpr int kRowsFlagWords = 480;
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;
@@ -80,6 +83,7 @@ struct DevCtx {
     uint64_t* o_part = nullptr;   // the same for the single-launch O (kFfnSlotWords)
     uint64_t* ofn_part = nullptr; // O's post-norm words of the single-launch O -> FFN (kOfnCopies x kFfnSlotWords)
     uint64_t* qkv_part = nullptr; // tagged per-head partial sums of the single-launch QKV (kQkvSlotWords)
+    uint64_t* rows_flag = nullptr; // tagged flags of the one-launch rows FFN (kRowsFlagWords)
     float* attn_part = nullptr;   // sliding_attention split partials (kAttnPartFloats)
     float* fattn_part = nullptr;  // full-attention page partials (kFattnPartFloats)
     void* base = nullptr;
@@ -89,6 +93,7 @@ struct DevCtx {
     int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
     int8_t full_o_fused[2] = {-1, -1};               // the same for full_attention_output
     int8_t o_ffn_fused[3] = {-1, -1, -1};            // the single-launch O -> FFN, per FFN format
+    int8_t rows_fused[6] = {-1, -1, -1, -1, -1, -1}; // the one-launch rows FFN, per (format, scale kind)
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.
@@ -126,6 +131,7 @@ struct Stall {
 };
 constexpr uint32_t kStealTicks = 50000;  // 500 us: far beyond any wait of a resident grid
 void set_stall(const Stall& st);           // the Stall every later single-launch call passes (tests)
+void set_rows_one_launch(bool on);         // the rows FFN's up/gate and down in one launch (default) or two (tests)
 
 struct FfnParams {
     FfnFormat fmt;

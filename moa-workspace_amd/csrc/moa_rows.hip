@@ -15,12 +15,19 @@
 //              L -> f32 partial sums [4][M][H]
 //   post       sum of the partials, the format's commit, post-RMSNorm, residual and layer scalar
 //              (rmsnorm.rs:204-296, residual.rs:189-241)
-// as four launches. (One launch with grid barriers between the steps, each step's weight loads
-// issued before its barrier, measured no faster: the barriers cost what the launches do.)
+// The pre-norm is a launch of its own; up/gate, down and post run in one launch
+// (rows_fused_kernel) where its grid fits on the device at once, with tagged flags between the
+// steps, else as three launches (rows_kernel twice, then chunk_post_rows_kernel), with the same
+// bits. (An earlier one-launch form with grid barriers between the steps, each step's first
+// weight loads issued before its barrier, measured no faster than the launches.)
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 
 #include "moa_device.h"
 #include "moa_internal.h"
+#include "moa_post_row.h"
+#include "moa_sync.h"
 
 namespace moa {
 namespace {
@@ -137,10 +144,12 @@ struct RwShape {
 
 // One wave's weight stream: a 16-row tile (GeGLU: of up and of gate) over one part of the
 // workgroup's k range KR, the FP4 block-scale codes of that range, and the ring of loads.
-template <FfnFormat F, bool G, int KR = kRwK>
+// DD: the ring's depth (the launch shape's by default; the one-launch kernel's down stream issues
+// DD - B steps ahead, up to all of them).
+template <FfnFormat F, bool G, int KR = kRwK, int DD = RwShape<F, G>::D>
 struct RwStream {
     static constexpr int NM = G ? 2 : 1;
-    static constexpr int NH = RwShape<F, G>::NH, D = RwShape<F, G>::D, B = RwShape<F, G>::B;
+    static constexpr int NH = RwShape<F, G>::NH, D = DD, B = RwShape<F, G>::B;
     static constexpr int LK = rw_lane_k<F>(), SKK = rw_step_k<F>();
     static constexpr int KW = KR / NH;    // k per wave
     static constexpr int S = KW / SKK;    // load steps per wave
@@ -155,10 +164,10 @@ struct RwStream {
 
 // The stream of lane (r, g) for weight rows n0 .. n0 + 15 of w0 (and w1), k kb .. kb + KW of rows
 // of wk elements: the scale codes, then the first D - B load steps.
-template <FfnFormat F, bool G, int KR>
-__device__ __forceinline__ void rw_prefetch(RwStream<F, G, KR>& st, const uint8_t* w0, const uint8_t* w1, const void* s0,
+template <FfnFormat F, bool G, int KR, int DD>
+__device__ __forceinline__ void rw_prefetch(RwStream<F, G, KR, DD>& st, const uint8_t* w0, const uint8_t* w1, const void* s0,
                                             const void* s1, int wk, int n0, int kb, int r, int g) {
-    using T = RwStream<F, G, KR>;
+    using T = RwStream<F, G, KR, DD>;
 #pragma unroll
     for (int k = 0; k < T::NM; ++k) {
         st.wp[k] = (k ? w1 : w0) + (size_t)(n0 + r) * (wk / T::EPB) + kb / T::EPB + 16 * g;
@@ -173,8 +182,10 @@ __device__ __forceinline__ void rw_prefetch(RwStream<F, G, KR>& st, const uint8_
     }
 #pragma unroll
     for (int i = 0; i < T::D - T::B; ++i)
+        if (i < T::S) {
 #pragma unroll
-        for (int k = 0; k < T::NM; ++k) st.ring[i][k] = rw_issue(st.wp[k], i);
+            for (int k = 0; k < T::NM; ++k) st.ring[i][k] = rw_issue(st.wp[k], i);
+        }
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rw_rsrc(const void* base, uint32_t bytes) {
@@ -243,10 +254,10 @@ __device__ __forceinline__ void rw_rows_store(const RwRows<NT, KR>& st, uint4* x
 // each step runs its MFMAs. MFMA j of a step takes the lane's k 8 j .. 8 j + 7 of its load -- for
 // A (LDS row r) and B alike, a fixed permutation of the step's k. acc[k][e]: row 4 g + e, weight
 // row r of the tile.
-template <FfnFormat F, bool G, int KR>
-__device__ __forceinline__ void rw_mma(RwStream<F, G, KR>& st, const uint4* xs, f32x4 (&acc)[G ? 2 : 1], int part, int r,
+template <FfnFormat F, bool G, int KR, int DD>
+__device__ __forceinline__ void rw_mma(RwStream<F, G, KR, DD>& st, const uint4* xs, f32x4 (&acc)[G ? 2 : 1], int part, int r,
                                        int g) {
-    using T = RwStream<F, G, KR>;
+    using T = RwStream<F, G, KR, DD>;
     constexpr int D = T::D, B = T::B, S = T::S;
 #pragma unroll
     for (int k = 0; k < T::NM; ++k) acc[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -306,9 +317,9 @@ __device__ __forceinline__ void rw_reduce(f32x4 (&acc)[NM], uint4* xs, int tile,
     }
 }
 
-// GeGLU of the up/gate sums for weight row n and rows 4 g + e < M into p [M][L].
+// GeGLU of the up/gate sums for weight row n: v[e] the bf16 bits of rows 4 g + e.
 template <FfnFormat F, ScaleKind SK>
-__device__ __forceinline__ void rw_geglu_out(const f32x4 (&acc)[2], const FfnParams& p, uint16_t* y, int n, int M, int g) {
+__device__ __forceinline__ void rw_geglu_vals(const f32x4 (&acc)[2], const FfnParams& p, int n, uint32_t (&v)[4]) {
     float su = 1.0f, sg = 1.0f;
     if constexpr (F == FfnFormat::FP8) {
         su = rw_row_scale<SK>(p.up_s, n);
@@ -319,11 +330,20 @@ __device__ __forceinline__ void rw_geglu_out(const f32x4 (&acc)[2], const FfnPar
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+        const float up = rw_commit<F>(acc[0][e], su), gate = rw_commit<F>(acc[1][e], sg);
+        v[e] = f2bf(rbf(gelu_tanh(gate)) * up);  // gemma4.py:197
+    }
+}
+
+// The same for rows 4 g + e < M into p [M][L].
+template <FfnFormat F, ScaleKind SK>
+__device__ __forceinline__ void rw_geglu_out(const f32x4 (&acc)[2], const FfnParams& p, uint16_t* y, int n, int M, int g) {
+    uint32_t v[4];
+    rw_geglu_vals<F, SK>(acc, p, n, v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
         const int m = 4 * g + e;
-        if (m < M) {
-            const float up = rw_commit<F>(acc[0][e], su), gate = rw_commit<F>(acc[1][e], sg);
-            y[(size_t)m * kL + n] = (uint16_t)f2bf(rbf(gelu_tanh(gate)) * up);  // gemma4.py:197
-        }
+        if (m < M) y[(size_t)m * kL + n] = (uint16_t)v[e];
     }
 }
 
@@ -363,6 +383,175 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
     else rw_partial_out(acc[0], yf, blockIdx.z, n0 + r, M, g);
 }
 
+// ---------------------------------------------------------------- up/gate and down in one launch
+// rows_fused_kernel runs the up/gate and the down launches of rows_kernel and the post launch as
+// one grid of kRwUpGroups workgroups, one per CU, all resident at once (the host checks the
+// occupancy first). Workgroup b computes the GeGLU block b (L columns 64 b .. +64, all rows) as
+// rows_kernel<GeGLU> does, then the down block (c, z) = (b % 60, b / 60) as rows_kernel<down>
+// does, and workgroup 15 m (m < M) then row m's post step as chunk_post_rows_kernel does: the
+// same arithmetic in the same order, so the same bits as the three launches.
+//
+// The hand-off of p: the workgroup writes its 16 x 64 GeGLU block with agent-scope 8-byte stores
+// (write-through, coherent across the XCDs' L2s), waits for them to complete, and then publishes
+// the launch's tag in its flag word. Down workgroup (c, z) needs the blocks of workgroups
+// 60 z .. 60 z + 59 (its quarter of L): one wave polls their 60 flags, then the workgroup stages
+// the quarter into LDS with ordinary loads. Those loads cannot meet a stale line: a kernel starts
+// with invalidated L2s, each block owns whole 128-byte lines, and no wave reads a block before its
+// flag carries the tag. The down weights (rw_down_pre steps per wave) go out right after the
+// publish (the waves that store no GeGLU value, before it), so they stream while the slowest
+// blocks are still being computed.
+//
+// The post step: every workgroup writes its down partial sums through (agent scope) and publishes
+// a second flag; leader 15 m polls all 240 of them and then reads row m's partials with ordinary
+// loads (the same argument as for p).
+//
+// Tags: the FFN's epoch counters (moa_sync.h epoch_tag), 16 workgroups per counter, shared with
+// the one-token FFN kernels, so consecutive launches of any of them never share a tag and a flag
+// left by an earlier launch never carries the current one. The poll is bounded by the wall clock
+// (kSpinTicks): on expiry it sets kErrSpinTimeout in the device error word and carries on. No
+// wait takes work over (as the one-token kernels' do): a grid that could not be resident would
+// end with that error rather than hang, and the host takes the three launches wherever the
+// occupancy check fails.
+//
+// Down steps per wave issued before p's quarter is staged (of 30 FP8, 15 FP4); the rest stream
+// behind the staging through the ring. Measured at 16 rows (graph-replayed): FP8 8 / 16 / 24 /
+// 30 steps 43.6 / 42.8 / 43.0 / 44.6 us; MXFP4 4 / 8 / 11 / 15 steps 31.4 / 30.6 / 30.7 / 31.7 us
+// (the staging loads return behind the prefetch, so a deeper prefetch delays the first MFMA).
+template <FfnFormat F>
+constexpr int rw_down_pre() { return F == FfnFormat::FP8 ? 16 : 8; }
+
+// The down partial sums of weight row n, split z, rows 4 g + e < M into yf [4][M][H], written
+// through (agent scope) for the leaders of the one-launch kernel.
+__device__ __forceinline__ void rw_partial_publish(const f32x4& acc, float* yf, int z, int n, int M, int g) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = 4 * g + e;
+        if (m < M) publish32(yf + ((size_t)z * M + m) * kH + n, __float_as_uint(acc[e]));
+    }
+}
+
+constexpr int kRwLeaderStride = kRwUpGroups / kMaxDecodeM;  // row m's post step on workgroup 15 m
+
+template <FfnFormat F, ScaleKind SK>
+__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, const uint16_t* x, int M, uint16_t* y,
+                                                                 float* yf, uint16_t* res, uint64_t* flags,
+                                                                 uint32_t* tickets, uint32_t* err) {
+    using TU = RwStream<F, true>;
+    using TD = RwStream<F, false, kRwK, rw_down_pre<F>() + RwShape<F, false>::B>;
+    constexpr int NW = 4 * kRwNH;
+    static_assert(kRwNH == 2 && kRwUpGroups == kFfnEpochCounters * kFfnEpochPer, "grid shape");
+    __shared__ __attribute__((aligned(16))) uint4 xs[rw_lds_units<kRwK>()];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int tile = wave & 3, part = wave >> 2;
+    const int r = lane & 15, g = lane >> 4;
+    const int b = blockIdx.x;
+    // the launch's epoch, needed only at the publish (its return arrives behind the first loads)
+    uint64_t ep_old = 0;
+    if (t == 0) ep_old = epoch_add(tickets + (kTicketFfnEpoch + b % kFfnEpochCounters) * kTicketStride);
+
+    // ---- up/gate (rows_kernel<GeGLU>)
+    f32x4 acc[2];
+    {
+        RwRows<64 * NW> rows;
+        rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
+        TU st;
+        rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, b * kRwGroupRows + tile * kRwTile,
+                                   part * TU::KW, r, g);
+        rw_rows_store(rows, xs, t);
+        rw_mma<F, true, kRwK>(st, xs, acc, part, r, g);
+    }
+    rw_reduce<2, kRwNH>(acc, xs, tile, part, lane);
+    // GeGLU block [16][64] into LDS past the reduction's floats, then out as 256 8-byte words
+    uint16_t* pb = reinterpret_cast<uint16_t*>(xs + 1024);
+    if (part == 0) {
+        uint32_t v[4];
+        rw_geglu_vals<F, SK>(acc, p, b * kRwGroupRows + tile * kRwTile + r, v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pb[(4 * g + e) * kRwGroupRows + tile * kRwTile + r] = (uint16_t)v[e];
+    }
+    rw_lds_barrier<-1>();
+    // ---- down (rows_kernel<down>): the weights first, then p's quarter once its blocks are in.
+    // Waves of part 1 store nothing, so their weights go out at once; waves of part 0 store the
+    // block, wait for their stores alone, and issue theirs after the flag.
+    constexpr int kPer = kRwUpGroups / kRwSplits;  // GeGLU blocks per quarter of L
+    static_assert(kMaxDecodeM * kRwGroupRows / 4 == 64 * (NW / 2), "one 8-byte word per thread of part 0");
+    const int c = b % kRwDownGroups, z = b / kRwDownGroups;
+    const int nd0 = c * kRwGroupRows + tile * kRwTile;
+    TD sd;
+    if (part != 0) {
+        rw_prefetch<F, false, kRwK>(sd, p.down, nullptr, p.down_s, nullptr, kL, nd0, z * kRwK + part * TD::KW, r, g);
+    } else {
+        const int m = t / (kRwGroupRows / 4), q = t % (kRwGroupRows / 4);
+        if (m < M)
+            publish64(reinterpret_cast<uint64_t*>(y + (size_t)m * kL + b * kRwGroupRows) + q,
+                      reinterpret_cast<const uint64_t*>(pb)[t]);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    const uint32_t tag = epoch_tag<kFfnEpochPer>(__shfl(ep_old, 0));  // wave 0: thread 0's epoch
+    if (t == 0) publish64(flags + b, tag);
+    if (part == 0)
+        rw_prefetch<F, false, kRwK>(sd, p.down, nullptr, p.down_s, nullptr, kL, nd0, z * kRwK + part * TD::KW, r, g);
+    if (wave == 0) {
+        const uint64_t* f = flags + z * kPer + (lane < kPer ? lane : 0);
+        const uint64_t t0 = wall_clock64();
+        while (!__all(collect64(f) == tag)) {
+            if (wall_clock64() - t0 > kSpinTicks) {
+                if (lane == 0) atomicOr(err, kErrSpinTimeout);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    rw_lds_barrier<-1>();
+    f32x4 dacc[1];
+    {
+        RwRows<64 * NW> rows;
+        rw_rows_load<64 * NW>(rows, y, kL, z * kRwK, M, t);
+        rw_rows_store(rows, xs, t);
+    }
+    rw_mma<F, false, kRwK>(sd, xs, dacc, part, r, g);
+    rw_reduce<1, kRwNH>(dacc, xs, tile, part, lane);
+
+    // ---- post: the partial sums out (written through), the block's down flag, and on leader
+    // workgroup 15 m (m < M) row m's post step once every down flag carries the tag -- post_row,
+    // as chunk_post_rows_kernel runs it (four waves; the other four have ended, and a barrier
+    // waits for the waves still running)
+    if (part == 0) {
+        rw_partial_publish(dacc[0], yf, z, nd0 + r, M, g);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (t == 0) publish64(flags + kRwUpGroups + b, tag);
+    const int m = b / kRwLeaderStride;
+    if (b % kRwLeaderStride != 0 || m >= M || part != 0) return;
+    if (wave == 0) {
+        const uint64_t t0 = wall_clock64();
+        for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < (kRwUpGroups + 63) / 64; ++i) {
+                const int k = lane + 64 * i;
+                if (k < kRwUpGroups) ok = ok && collect64(flags + kRwUpGroups + k) == tag;
+            }
+            if (__all(ok)) break;
+            if (wall_clock64() - t0 > kSpinTicks) {
+                if (lane == 0) atomicOr(err, kErrSpinTimeout);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    uint4 out[2];
+    post_row<SK, F, kRwSplits>(yf, kRwSplits, M, F == FfnFormat::FP8 ? p.down_s : nullptr,
+                               F == FfnFormat::NVFP4 ? p.down_g : nullptr, p.post_rms, res, p.layer_scalar, m,
+                               reinterpret_cast<float*>(xs), out);
+}
+
 // ---------------------------------------------------------------- host
 template <FfnFormat F, ScaleKind SK, bool G>
 hipError_t rw_launch(dim3 grid, hipStream_t s, const FfnParams& p, const uint16_t* x, int ldx, int M, uint16_t* y, float* yf) {
@@ -370,11 +559,33 @@ hipError_t rw_launch(dim3 grid, hipStream_t s, const FfnParams& p, const uint16_
     return hipGetLastError();
 }
 
+std::atomic<int> g_rows_one_launch{1};
+
+// Whether rows_fused_kernel runs: its hand-off words exist, tests have not switched it off, and its
+// grid fits on the device at once (checked once per device and format).
+template <FfnFormat F, ScaleKind SK>
+bool rows_fused_fits(DevCtx* ctx) {
+    if (!ctx->rows_flag || !g_rows_one_launch.load()) return false;
+    int8_t& known = ctx->rows_fused[(int)F * 2 + (int)SK];
+    if (known < 0) {
+        int per_cu = 0;
+        const hipError_t e =
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rows_fused_kernel<F, SK>, 256 * kRwNH, 0);
+        known = (e == hipSuccess && per_cu * ctx->cus >= kRwUpGroups) ? 1 : 0;
+    }
+    return known == 1;
+}
+
 // normed: the pre-norm's rows are already in ctx->hbuf (launch_o_ffn_rows)
 template <FfnFormat F, ScaleKind SK>
 hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed = false) {
     hipError_t e = normed ? hipSuccess : launch_rmsnorm_rows(p.residual + (size_t)m0 * kH, p.pre_rms, ctx->hbuf, M, s);
     if (e != hipSuccess) return e;
+    if (rows_fused_fits<F, SK>(ctx)) {
+        hipLaunchKernelGGL((rows_fused_kernel<F, SK>), dim3(kRwUpGroups), dim3(256 * kRwNH), 0, s, p, ctx->hbuf, M,
+                           ctx->pbuf, ctx->fbuf, p.residual + (size_t)m0 * kH, ctx->rows_flag, ctx->tickets, ctx->err);
+        return hipGetLastError();
+    }
     e = rw_launch<F, SK, true>(dim3(kRwUpGroups, 1, 1), s, p, ctx->hbuf, kH, M, ctx->pbuf, nullptr);
     if (e != hipSuccess) return e;
     e = rw_launch<F, SK, false>(dim3(kRwDownGroups, 1, kRwSplits), s, p, ctx->pbuf, kL, M, nullptr, ctx->fbuf);
@@ -583,5 +794,7 @@ hipError_t launch_o_ffn_rows(const OParams& o, const FfnParams& p, int m0, int M
     if (e != hipSuccess) return e;
     return ffn_rows_dispatch(p, m0, M, s, ctx, true);
 }
+
+void set_rows_one_launch(bool on) { g_rows_one_launch.store(on ? 1 : 0); }
 
 }  // namespace moa

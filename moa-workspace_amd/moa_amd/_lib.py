@@ -81,6 +81,7 @@ SIGNATURES = {
     "moa_test_preset_epochs": [U64],
     "moa_test_set_stall": [C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)],
     "moa_test_take_overs": [U32P],
+    "moa_test_set_rows_one_launch": [C.c_int],
     "moa_test_scratch_state": [U32P],
     "moa_test_trip_device_state": [I32],
     "moa_clear_device_state": [I32],

@@ -57,6 +57,35 @@ def test_rows_are_independent_and_repeatable(fmt):
     assert np.array_equal(a, got(d16))
 
 
+def _rows_one_launch(on: bool) -> None:
+    import ctypes as C
+    from moa_amd import _lib
+    _lib.call("moa_test_set_rows_one_launch", C.c_int(1 if on else 0))
+
+
+@pytest.mark.parametrize("M", [2, 9, 16])
+@pytest.mark.parametrize("fmt", ["fp8", "nvfp4", "mxfp4"])
+def test_one_launch_equals_two_launches(fmt, M):
+    """The up/gate and down contractions in one launch (rows_fused_kernel, the default where its
+    grid fits) give the bits of the two launches. Four calls in a row, each on other rows: a GeGLU
+    block read before its producer had written it, or a stale copy of an earlier call's, would
+    show as a difference."""
+    need_gpu()
+    say(f"ffn rows {fmt} M{M}: one launch vs two")
+    from moa_amd import ops
+    _, got = FORMATS[fmt]
+    ds = [case(fmt, M, f"launches{i}") for i in range(4)]
+    one = [got(d) for d in ds]
+    _rows_one_launch(False)
+    try:
+        two = [got(d) for d in ds]
+    finally:
+        _rows_one_launch(True)
+    for i, (a, b) in enumerate(zip(one, two)):
+        assert np.array_equal(a, b), f"call {i}: {int(np.sum(a != b))} outputs differ"
+    assert ops.device_errors() == 0
+
+
 @pytest.mark.parametrize("fmt", ["nvfp4", "mxfp4"])
 def test_fp4_calls_of_17_rows(fmt):
     """17 rows: the first call length past the rows path (the MFMA path, a partial row tile)."""
