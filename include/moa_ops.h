@@ -276,17 +276,17 @@ int moa_fp8_scaled_projection(const uint16_t* x, const uint8_t* w, const float* 
  * kernels' own device helpers into out (device uint32 [721924]; layout in moa_decode.hip). */
 int moa_format_selftest(uint32_t* out, void* stream);
 
-/* Test support for the launch epochs of the one-token kernels (no counterpart in the reference).
- * The one-token QKV (kernel 0), O (1) and FFN (2) kernels tag their cross-workgroup hand-off
- * words with a per-launch tag derived from 64-bit epoch counters that `per` workgroups of each
- * launch advance by one. moa_test_epoch_layout gives the number of counters and `per`;
+/* Test support for the launch epochs of the one-launch kernels (no counterpart in the reference).
+ * The one-token QKV (kernel 0), O (1) and FFN (2) kernels and the FFN of 2..16 rows (3) tag their
+ * cross-workgroup hand-off words with a per-launch tag derived from 64-bit epoch counters that
+ * `per` workgroups of each launch advance by one. moa_test_epoch_layout gives the number of counters and `per`;
  * moa_test_epoch_tag computes, on the host, the tag a workgroup derives from the value `old` its
  * add returned (the same function the kernels run). Neither touches a device. */
 int moa_test_epoch_layout(int kernel, int* counters, int* per);
 int moa_test_epoch_tag(int kernel, uint64_t old, uint32_t* tag);
 
 /* Test support: sets every epoch counter of the current device as if `launches` launches of each
- * one-token kernel had run (counter = launches * per), and the sliding-attention tickets to
+ * one-launch kernel had run (counter = launches * per), and the sliding-attention tickets to
  * (launches * 32) mod 2^32, so that a test can cross counter wrap points without running
  * billions of launches. Synchronous; no call may be in flight on the device. */
 int moa_test_preset_epochs(uint64_t launches);

@@ -654,8 +654,9 @@ int moa_test_epoch_layout(int kernel, int* counters, int* per) {
         case 0: *counters = kQkvEpochCounters; *per = kQkvEpochPer; return MOA_SUCCESS;
         case 1: *counters = kOEpochCounters; *per = kOEpochPer; return MOA_SUCCESS;
         case 2: *counters = kFfnEpochCounters; *per = kFfnEpochPer; return MOA_SUCCESS;
+        case 3: *counters = kRowsEpochCounters; *per = kRowsEpochPer; return MOA_SUCCESS;
     }
-    return fail(MOA_ERROR_INVALID_VALUE, "kernel must be 0 (QKV), 1 (O) or 2 (FFN)");
+    return fail(MOA_ERROR_INVALID_VALUE, "kernel must be 0 (QKV), 1 (O), 2 (FFN) or 3 (rows FFN)");
 }
 
 int moa_test_epoch_tag(int kernel, uint64_t old, uint32_t* tag) {
@@ -664,8 +665,9 @@ int moa_test_epoch_tag(int kernel, uint64_t old, uint32_t* tag) {
         case 0: *tag = epoch_tag<kQkvEpochPer>(old); return MOA_SUCCESS;
         case 1: *tag = epoch_tag<kOEpochPer>(old); return MOA_SUCCESS;
         case 2: *tag = epoch_tag<kFfnEpochPer>(old); return MOA_SUCCESS;
+        case 3: *tag = epoch_tag<kRowsEpochPer>(old); return MOA_SUCCESS;
     }
-    return fail(MOA_ERROR_INVALID_VALUE, "kernel must be 0 (QKV), 1 (O) or 2 (FFN)");
+    return fail(MOA_ERROR_INVALID_VALUE, "kernel must be 0 (QKV), 1 (O), 2 (FFN) or 3 (rows FFN)");
 }
 
 int moa_test_preset_epochs(uint64_t launches) {
@@ -680,6 +682,7 @@ int moa_test_preset_epochs(uint64_t launches) {
     put64(kTicketQkvEpoch, kQkvEpochCounters, launches * kQkvEpochPer);
     put64(kTicketOEpoch, kOEpochCounters, launches * kOEpochPer);
     put64(kTicketFfnEpoch, kFfnEpochCounters, launches * kFfnEpochPer);
+    put64(kTicketRowsEpoch, kRowsEpochCounters, launches * kRowsEpochPer);
     const uint32_t at = (uint32_t)(launches * 32u);
     for (int i = 0; i < kMaxDecodeM * kNs && e == hipSuccess; ++i)
         e = hipMemcpy(ctx->tickets + (size_t)(kTicketAttn + i) * kTicketStride, &at, sizeof at, hipMemcpyHostToDevice);

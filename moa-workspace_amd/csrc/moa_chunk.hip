@@ -490,19 +490,10 @@ template <bool Tiles>
 __device__ __forceinline__ void rms_row_store(const float (&xv)[16], const float (&wv)[16], int m, float* red,
                                               uint16_t* __restrict__ out) {
     const int t = threadIdx.x;
-    const bool act = t < kH / 16;
     const int c = min(t, kH / 16 - 1);
-    float ss = 0.0f;
-    if (act) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);
-    }
-    const float inv = rms_inverse(ck_block_sum(ss, red), kH);
-    if (!act) return;
     uint32_t h[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        h[i] = pk_bf16((xv[2 * i] * inv) * wv[2 * i], (xv[2 * i + 1] * inv) * wv[2 * i + 1]);
+    rms_row_values(xv, wv, red, h);
+    if (t >= kH / 16) return;
     const size_t o0 = Tiles ? atile_off(m, c * 16, kH) : (size_t)m * kH + c * 16;
     const size_t o1 = Tiles ? atile_off(m, c * 16 + 8, kH) : (size_t)m * kH + c * 16 + 8;
     *reinterpret_cast<uint4*>(out + o0) = make_uint4(h[0], h[1], h[2], h[3]);

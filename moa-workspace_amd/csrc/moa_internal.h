@@ -40,7 +40,9 @@ constexpr int kOEpochCounters = 15, kOEpochPer = 16;
 constexpr int kQkvEpochCounters = 32, kQkvEpochPer = 8;
 constexpr int kFfnEpochCounters = 15, kFfnEpochPer = 16;
 // sliding_attention: one counter per (row, head) of a launch, 32 arrivals per launch, never reset
-constexpr int kTicketAttn = kTicketFfnEpoch + 16;
+constexpr int kTicketRowsEpoch = kTicketFfnEpoch + 16;  // the one-launch rows FFN (16 of 16)
+constexpr int kRowsEpochCounters = 16, kRowsEpochPer = 16;
+constexpr int kTicketAttn = kTicketRowsEpoch + 16;
 constexpr int kTicketCount = kTicketAttn + kMaxDecodeM * kNs;
 // sliding_attention partials: [kMaxDecodeM][kNs][32 chunks][kGs][max, sum, o[kDs]]
 constexpr size_t kAttnPartFloats = (size_t)kMaxDecodeM * kNs * 32 * kGs * (4 + kDs);
@@ -60,8 +62,8 @@ constexpr int kFfnSlotWords = kFfnPartSlots * 10;
 constexpr int kQkvSlotWords = 32 * 8;
 constexpr int kOfnCopies = 8;  // copies of O's post-norm words in the single-launch O -> FFN kernel
 // Tagged flags of the one-launch rows FFN (moa_rows.hip rows_fused_kernel): one per GeGLU block,
-// then one per block of down partial sums.
-constexpr int kRowsFlagWords = 480;
+// one per block of down partial sums, one per normalised row.
+constexpr int kRowsFlagWords = 512;
 
 // Device-side error bits (OR-ed by kernels; read back by moa_device_errors()).
 constexpr uint32_t kErrRopeOffset = 1u;

@@ -27,6 +27,22 @@ __device__ __forceinline__ float ck_block_sum(float v, float* red) {
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
+// Row RMSNorm by four waves: thread t < kH / 16 holds elements 16 t .. 16 t + 15 of the row (xv)
+// and their weights (wv); h receives the 8 bf16 pairs of bf16(x * inv * w) (gemma4.py:83-89).
+// Threads past the row take part in the sum with nothing.
+__device__ __forceinline__ void rms_row_values(const float (&xv)[16], const float (&wv)[16], float* red, uint32_t (&h)[8]) {
+    const bool act = threadIdx.x < kH / 16;
+    float ss = 0.0f;
+    if (act) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ss = fmaf(xv[i], xv[i], ss);
+    }
+    const float inv = rms_inverse(ck_block_sum(ss, red), kH);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        h[i] = pk_bf16((xv[2 * i] * inv) * wv[2 * i], (xv[2 * i + 1] * inv) * wv[2 * i + 1]);
+}
+
 // Per row: d = bf16((sum of the split-K partials) * s[n]), then out = bf16(bf16(r + N(d)) * ls)
 // with N the post-RMSNorm (identity when w_post is null) and ls skipped when null
 // (shared/rmsnorm.rs:204-296, residual.rs:189-241; generate_references.py:411-413).

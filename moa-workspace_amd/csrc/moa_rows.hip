@@ -384,12 +384,17 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
 }
 
 // ---------------------------------------------------------------- up/gate and down in one launch
-// rows_fused_kernel runs the up/gate and the down launches of rows_kernel and the post launch as
-// one grid of kRwUpGroups workgroups, one per CU, all resident at once (the host checks the
-// occupancy first). Workgroup b computes the GeGLU block b (L columns 64 b .. +64, all rows) as
-// rows_kernel<GeGLU> does, then the down block (c, z) = (b % 60, b / 60) as rows_kernel<down>
-// does, and workgroup 15 m (m < M) then row m's post step as chunk_post_rows_kernel does: the
-// same arithmetic in the same order, so the same bits as the three launches.
+// rows_fused_kernel runs the pre-norm, the up/gate and down launches of rows_kernel and the post
+// launch as one grid of kRwFusedGrid workgroups, one per CU, all resident at once (the host checks
+// the occupancy first): 16 service workgroups and 240 contraction workgroups.
+//   * Service workgroup m < M normalises residual row m as chunk_rmsnorm_rows_kernel<false> does
+//     (four waves, the same arithmetic through rms_row_values), writes it through and flags it;
+//     at the end it runs row m's post step as chunk_post_rows_kernel does (post_row).
+//   * Contraction workgroup b issues its first up/gate weight loads, waits for the M row flags,
+//     stages the rows, and computes the GeGLU block b (L columns 64 b .. +64, all rows) as
+//     rows_kernel<GeGLU> does, then the down block (c, z) = (b % 60, b / 60) as rows_kernel<down>
+//     does.
+// The same arithmetic in the same order as the separate launches, so the same bits.
 //
 // The hand-off of p: the workgroup writes its 16 x 64 GeGLU block with agent-scope 8-byte stores
 // (write-through, coherent across the XCDs' L2s), waits for them to complete, and then publishes
@@ -397,21 +402,19 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
 // 60 z .. 60 z + 59 (its quarter of L): one wave polls their 60 flags, then the workgroup stages
 // the quarter into LDS with ordinary loads. Those loads cannot meet a stale line: a kernel starts
 // with invalidated L2s, each block owns whole 128-byte lines, and no wave reads a block before its
-// flag carries the tag. The down weights (rw_down_pre steps per wave) go out right after the
-// publish (the waves that store no GeGLU value, before it), so they stream while the slowest
-// blocks are still being computed.
+// flag carries the tag. The normalised rows and the down partial sums go the same way: written
+// through, flagged, and read with ordinary loads once flagged (the rows by every contraction
+// workgroup, row m's partials by service workgroup m). The down weights (rw_down_pre steps per
+// wave) go out right after the GeGLU publish (the waves that store no GeGLU value, before it),
+// so they stream while the slowest blocks are still being computed.
 //
-// The post step: every workgroup writes its down partial sums through (agent scope) and publishes
-// a second flag; leader 15 m polls all 240 of them and then reads row m's partials with ordinary
-// loads (the same argument as for p).
-//
-// Tags: the FFN's epoch counters (moa_sync.h epoch_tag), 16 workgroups per counter, shared with
-// the one-token FFN kernels, so consecutive launches of any of them never share a tag and a flag
-// left by an earlier launch never carries the current one. The poll is bounded by the wall clock
-// (kSpinTicks): on expiry it sets kErrSpinTimeout in the device error word and carries on. No
-// wait takes work over (as the one-token kernels' do): a grid that could not be resident would
-// end with that error rather than hang, and the host takes the three launches wherever the
-// occupancy check fails.
+// Tags: epoch counters of this kernel alone (moa_sync.h epoch_tag), 16 workgroups per counter, so
+// consecutive launches never share a tag and a flag left by an earlier launch never carries the
+// current one. Every poll is bounded by the wall clock (kSpinTicks): on expiry it sets
+// kErrSpinTimeout in the device error word and carries on. No wait takes work over (as the
+// one-token kernels' do): a grid that could not be resident would end with that error rather than
+// hang, and the host takes the separate launches wherever the occupancy check fails. The service
+// workgroups' four upper waves end at once; their barriers then wait for the four that remain.
 //
 // Down steps per wave issued before p's quarter is staged (of 30 FP8, 15 FP4); the rest stream
 // behind the staging through the ring. Measured at 16 rows (graph-replayed): FP8 8 / 16 / 24 /
@@ -419,6 +422,12 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
 // (the staging loads return behind the prefetch, so a deeper prefetch delays the first MFMA).
 template <FfnFormat F>
 constexpr int rw_down_pre() { return F == FfnFormat::FP8 ? 16 : 8; }
+
+// The up/gate ring's depth (D - 4 steps go out before the rows are staged). Measured at 16 rows:
+// 8 / 12 / 16 steps FP8 42.8 / 41.1 / 41.0 us, MXFP4 30.0 / 29.6 / 30.7 us. (The pre-norm as a
+// launch of its own ahead of this kernel measured 43.4 / 31.6 us at depth 8.)
+template <FfnFormat F>
+constexpr int rw_ug_depth() { return F == FfnFormat::FP8 ? 16 : 12; }
 
 // The down partial sums of weight row n, split z, rows 4 g + e < M into yf [4][M][H], written
 // through (agent scope) for the leaders of the one-launch kernel.
@@ -430,33 +439,103 @@ __device__ __forceinline__ void rw_partial_publish(const f32x4& acc, float* yf, 
     }
 }
 
-constexpr int kRwLeaderStride = kRwUpGroups / kMaxDecodeM;  // row m's post step on workgroup 15 m
+constexpr int kRwService = kMaxDecodeM;                 // workgroups 0 .. 15: row m's pre-norm and post step
+constexpr int kRwFusedGrid = kRwService + kRwUpGroups;  // and 240 contraction workgroups
+static_assert(kRwFusedGrid == kRowsEpochCounters * kRowsEpochPer, "equal workgroups per epoch counter");
+// flag words: the GeGLU blocks, the down blocks, the normalised rows
+constexpr int kRwFlagP = 0, kRwFlagDown = kRwUpGroups, kRwFlagNorm = 2 * kRwUpGroups;
+static_assert(kRwFlagNorm + kMaxDecodeM <= kRowsFlagWords, "flag words");
 
+// Polls flags[first + i], i < n (n <= 256), until every one carries tag; one wave.
+__device__ __forceinline__ void rw_poll(const uint64_t* flags, int first, int n, uint32_t tag, uint32_t* err, int lane) {
+    const uint64_t t0 = wall_clock64();
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = lane + 64 * i;
+            if (k < n) ok = ok && collect64(flags + first + k) == tag;
+        }
+        if (__all(ok)) return;
+        if (wall_clock64() - t0 > kSpinTicks) {
+            if (lane == 0) atomicOr(err, kErrSpinTimeout);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// res: the M residual rows; x: their normalised rows, which the service workgroups write first when
+// norm is set (else they are there already).
 template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, const uint16_t* x, int M, uint16_t* y,
+__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, bool norm, uint16_t* x, int M, uint16_t* y,
                                                                  float* yf, uint16_t* res, uint64_t* flags,
                                                                  uint32_t* tickets, uint32_t* err) {
-    using TU = RwStream<F, true>;
+    using TU = RwStream<F, true, kRwK, rw_ug_depth<F>()>;
     using TD = RwStream<F, false, kRwK, rw_down_pre<F>() + RwShape<F, false>::B>;
     constexpr int NW = 4 * kRwNH;
-    static_assert(kRwNH == 2 && kRwUpGroups == kFfnEpochCounters * kFfnEpochPer, "grid shape");
+    static_assert(kRwNH == 2, "grid shape");
     __shared__ __attribute__((aligned(16))) uint4 xs[rw_lds_units<kRwK>()];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int tile = wave & 3, part = wave >> 2;
     const int r = lane & 15, g = lane >> 4;
-    const int b = blockIdx.x;
-    // the launch's epoch, needed only at the publish (its return arrives behind the first loads)
+    // the launch's epoch (its return arrives behind the first loads; wave 0 derives the tag)
     uint64_t ep_old = 0;
-    if (t == 0) ep_old = epoch_add(tickets + (kTicketFfnEpoch + b % kFfnEpochCounters) * kTicketStride);
+    if (t == 0) ep_old = epoch_add(tickets + (kTicketRowsEpoch + blockIdx.x % kRowsEpochCounters) * kTicketStride);
 
-    // ---- up/gate (rows_kernel<GeGLU>)
+    // ---- service workgroup m: the pre-norm of row m, then its post step (four waves)
+    if (blockIdx.x < kRwService) {
+        const int m = blockIdx.x;
+        if (m >= M || part != 0) return;
+        float* red = reinterpret_cast<float*>(xs);
+        const uint32_t tag = epoch_tag<kRowsEpochPer>(__shfl(ep_old, 0));
+        if (norm) {
+            // chunk_rmsnorm_rows_kernel's arithmetic, its row written through (agent scope)
+            const int c = min(t, kH / 16 - 1);
+            const uint16_t* xr = res + (size_t)m * kH + c * 16;
+            float xv[16], wv[16];
+            bf16x8_to_f32(ld16(xr), xv);
+            bf16x8_to_f32(ld16(xr + 8), xv + 8);
+            bf16x8_to_f32(ld16(p.pre_rms + c * 16), wv);
+            bf16x8_to_f32(ld16(p.pre_rms + c * 16 + 8), wv + 8);
+            uint32_t h[8];
+            rms_row_values(xv, wv, red, h);
+            if (t < kH / 16) {
+                uint64_t* o = reinterpret_cast<uint64_t*>(x + (size_t)m * kH + c * 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) publish64(o + i, ((uint64_t)h[2 * i + 1] << 32) | h[2 * i]);
+            }
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (t == 0) publish64(flags + kRwFlagNorm + m, tag);
+        }
+        if (wave == 0) rw_poll(flags, kRwFlagDown, kRwUpGroups, tag, err, lane);
+        __syncthreads();
+        uint4 out[2];
+        post_row<SK, F, kRwSplits>(yf, kRwSplits, M, F == FfnFormat::FP8 ? p.down_s : nullptr,
+                                   F == FfnFormat::NVFP4 ? p.down_g : nullptr, p.post_rms, res, p.layer_scalar, m, red,
+                                   out);
+        return;
+    }
+
+    // ---- contraction workgroup b: up/gate (rows_kernel<GeGLU>)
+    const int b = blockIdx.x - kRwService;
+    const uint32_t tag = epoch_tag<kRowsEpochPer>(__shfl(ep_old, 0));  // valid in wave 0
     f32x4 acc[2];
     {
+        const int n0 = b * kRwGroupRows + tile * kRwTile;
         RwRows<64 * NW> rows;
-        rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
         TU st;
-        rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, b * kRwGroupRows + tile * kRwTile,
-                                   part * TU::KW, r, g);
+        if (norm) {
+            // the weights first; the rows once the service workgroups have published them
+            rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, part * TU::KW, r, g);
+            if (wave == 0) rw_poll(flags, kRwFlagNorm, M, tag, err, lane);
+            rw_lds_barrier<-1>();
+            rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
+        } else {
+            rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
+            rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, part * TU::KW, r, g);
+        }
         rw_rows_store(rows, xs, t);
         rw_mma<F, true, kRwK>(st, xs, acc, part, r, g);
     }
@@ -489,21 +568,10 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, co
     }
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    const uint32_t tag = epoch_tag<kFfnEpochPer>(__shfl(ep_old, 0));  // wave 0: thread 0's epoch
-    if (t == 0) publish64(flags + b, tag);
+    if (t == 0) publish64(flags + kRwFlagP + b, tag);
     if (part == 0)
         rw_prefetch<F, false, kRwK>(sd, p.down, nullptr, p.down_s, nullptr, kL, nd0, z * kRwK + part * TD::KW, r, g);
-    if (wave == 0) {
-        const uint64_t* f = flags + z * kPer + (lane < kPer ? lane : 0);
-        const uint64_t t0 = wall_clock64();
-        while (!__all(collect64(f) == tag)) {
-            if (wall_clock64() - t0 > kSpinTicks) {
-                if (lane == 0) atomicOr(err, kErrSpinTimeout);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
+    if (wave == 0) rw_poll(flags, kRwFlagP + z * kPer, kPer, tag, err, lane);
     rw_lds_barrier<-1>();
     f32x4 dacc[1];
     {
@@ -513,43 +581,14 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, co
     }
     rw_mma<F, false, kRwK>(sd, xs, dacc, part, r, g);
     rw_reduce<1, kRwNH>(dacc, xs, tile, part, lane);
-
-    // ---- post: the partial sums out (written through), the block's down flag, and on leader
-    // workgroup 15 m (m < M) row m's post step once every down flag carries the tag -- post_row,
-    // as chunk_post_rows_kernel runs it (four waves; the other four have ended, and a barrier
-    // waits for the waves still running)
+    // ---- the partial sums out (written through), then the block's down flag
     if (part == 0) {
         rw_partial_publish(dacc[0], yf, z, nd0 + r, M, g);
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
-    if (t == 0) publish64(flags + kRwUpGroups + b, tag);
-    const int m = b / kRwLeaderStride;
-    if (b % kRwLeaderStride != 0 || m >= M || part != 0) return;
-    if (wave == 0) {
-        const uint64_t t0 = wall_clock64();
-        for (;;) {
-            bool ok = true;
-#pragma unroll
-            for (int i = 0; i < (kRwUpGroups + 63) / 64; ++i) {
-                const int k = lane + 64 * i;
-                if (k < kRwUpGroups) ok = ok && collect64(flags + kRwUpGroups + k) == tag;
-            }
-            if (__all(ok)) break;
-            if (wall_clock64() - t0 > kSpinTicks) {
-                if (lane == 0) atomicOr(err, kErrSpinTimeout);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-    uint4 out[2];
-    post_row<SK, F, kRwSplits>(yf, kRwSplits, M, F == FfnFormat::FP8 ? p.down_s : nullptr,
-                               F == FfnFormat::NVFP4 ? p.down_g : nullptr, p.post_rms, res, p.layer_scalar, m,
-                               reinterpret_cast<float*>(xs), out);
+    if (t == 0) publish64(flags + kRwFlagDown + b, tag);
 }
 
 // ---------------------------------------------------------------- host
@@ -571,7 +610,7 @@ bool rows_fused_fits(DevCtx* ctx) {
         int per_cu = 0;
         const hipError_t e =
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rows_fused_kernel<F, SK>, 256 * kRwNH, 0);
-        known = (e == hipSuccess && per_cu * ctx->cus >= kRwUpGroups) ? 1 : 0;
+        known = (e == hipSuccess && per_cu * ctx->cus >= kRwFusedGrid) ? 1 : 0;
     }
     return known == 1;
 }
@@ -579,13 +618,13 @@ bool rows_fused_fits(DevCtx* ctx) {
 // normed: the pre-norm's rows are already in ctx->hbuf (launch_o_ffn_rows)
 template <FfnFormat F, ScaleKind SK>
 hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed = false) {
-    hipError_t e = normed ? hipSuccess : launch_rmsnorm_rows(p.residual + (size_t)m0 * kH, p.pre_rms, ctx->hbuf, M, s);
-    if (e != hipSuccess) return e;
     if (rows_fused_fits<F, SK>(ctx)) {
-        hipLaunchKernelGGL((rows_fused_kernel<F, SK>), dim3(kRwUpGroups), dim3(256 * kRwNH), 0, s, p, ctx->hbuf, M,
-                           ctx->pbuf, ctx->fbuf, p.residual + (size_t)m0 * kH, ctx->rows_flag, ctx->tickets, ctx->err);
+        hipLaunchKernelGGL((rows_fused_kernel<F, SK>), dim3(kRwFusedGrid), dim3(256 * kRwNH), 0, s, p, !normed, ctx->hbuf,
+                           M, ctx->pbuf, ctx->fbuf, p.residual + (size_t)m0 * kH, ctx->rows_flag, ctx->tickets, ctx->err);
         return hipGetLastError();
     }
+    hipError_t e = normed ? hipSuccess : launch_rmsnorm_rows(p.residual + (size_t)m0 * kH, p.pre_rms, ctx->hbuf, M, s);
+    if (e != hipSuccess) return e;
     e = rw_launch<F, SK, true>(dim3(kRwUpGroups, 1, 1), s, p, ctx->hbuf, kH, M, ctx->pbuf, nullptr);
     if (e != hipSuccess) return e;
     e = rw_launch<F, SK, false>(dim3(kRwDownGroups, 1, kRwSplits), s, p, ctx->pbuf, kL, M, nullptr, ctx->fbuf);

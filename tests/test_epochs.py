@@ -1,7 +1,7 @@
 """Launch epochs of the one-token kernels, modelled on the CPU through the library's own tag
 function (moa_test_epoch_tag runs the code the kernels run; no device is touched).
 
-A one-token QKV, O or FFN launch tags its cross-workgroup hand-off words with a tag that every
+A one-token QKV, O or FFN launch (and the FFN of 2..16 rows) tags its cross-workgroup hand-off words with a tag that every
 workgroup derives from the value its add to a 64-bit epoch counter returned. The model replays
 launches in which the workgroups add in arbitrary orders and checks, around every wrap point a
 counter or a tag could reach, that (1) all workgroups of a launch derive the same tag, (2) the tag
@@ -16,8 +16,8 @@ import pytest
 
 from moa_amd import _lib
 
-KERNELS = {0: "qkv", 1: "o", 2: "ffn"}
-GRID = {0: 256, 1: 240, 2: 240}  # workgroups of the one-token launches
+KERNELS = {0: "qkv", 1: "o", 2: "ffn", 3: "rows ffn"}
+GRID = {0: 256, 1: 240, 2: 240, 3: 256}  # workgroups of the one-launch kernels
 
 
 def layout(kernel):
@@ -58,7 +58,7 @@ def replay(kernel, start_launches, launches, seed, width=64):
 WRAPS = [0, 2**28 - 3, 2**29 - 3, 2**32 - 4, 2**32 // 15 - 2, 2**60 // 16 - 3]
 
 
-@pytest.mark.parametrize("kernel", [0, 1, 2])
+@pytest.mark.parametrize("kernel", [0, 1, 2, 3])
 @pytest.mark.parametrize("start", WRAPS)
 def test_every_launch_agrees_and_differs_from_the_last(kernel, start):
     tags = replay(kernel, start, 7, seed=start ^ kernel)
@@ -103,6 +103,6 @@ def test_former_scheme_breaks_at_the_32_bit_wrap():
 def test_bad_kernel_index_is_rejected():
     lib = _lib.load()
     t = C.c_uint32()
-    assert lib.moa_test_epoch_tag(3, 0, C.byref(t)) == -1
+    assert lib.moa_test_epoch_tag(4, 0, C.byref(t)) == -1
     n, per = C.c_int(), C.c_int()
     assert lib.moa_test_epoch_layout(-1, C.byref(n), C.byref(per)) == -1

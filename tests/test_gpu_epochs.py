@@ -1,5 +1,5 @@
 """Launch epochs across their wrap points on the device. The epoch counters of the one-token
-QKV, O and FFN kernels (and the sliding-attention tickets) are preset by the test hook as if
+QKV, O and FFN kernels and of the 16-row FFN (and the sliding-attention tickets) are preset by the test hook as if
 2^27 - 2, 2^28 - 2 or 2^32 - 3 launches had run; four launches of each operator then cross:
 the 32-bit wrap of the attention tickets (2^27 launches x 32 arrivals), the 32-bit boundary of the
 64-bit FFN / O counters (2^28 launches x 16 workgroups), and the wrap of the 32-bit tag itself
@@ -44,6 +44,15 @@ def calls():
                                     ft["post_ff_rms_weight"], ft["layer_scalar"])
         return host(r)
 
+    r16 = dev(synth.bf16_normal("epochs.rows16", (16, 3840)))
+
+    def ffn_rows():
+        r = r16.clone()
+        ops.decoder_feedforward_fp8(r, ft["pre_ff_rms_weight"], ft["up_weight"], ft["gate_weight"], ft["down_weight"],
+                                    ft["up_weight_scale"], ft["gate_weight_scale"], ft["down_weight_scale"],
+                                    ft["post_ff_rms_weight"], ft["layer_scalar"])
+        return host(r)
+
     def o_proj():
         r = ot["residual"].clone()
         ops.sliding_attention_output(ot["x"], ot["post_attn_rms_weight"], ot["o_weight"], ot["o_weight_scale"], r)
@@ -61,7 +70,7 @@ def calls():
         ops.sliding_attention(at["q"], at["k_cache"], at["v_cache"], at["mask"], out)
         return host(out)
 
-    return {"ffn": ffn, "o": o_proj, "qkv": qkv, "attention": attn}
+    return {"ffn": ffn, "ffn_rows": ffn_rows, "o": o_proj, "qkv": qkv, "attention": attn}
 
 
 @pytest.mark.parametrize("start", [2**27 - 2, 2**28 - 2, 2**32 - 3])
