@@ -386,10 +386,12 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
 // ---------------------------------------------------------------- up/gate and down in one launch
 // rows_fused_kernel runs the pre-norm, the up/gate and down launches of rows_kernel and the post
 // launch as one grid of kRwFusedGrid workgroups, one per CU, all resident at once (the host checks
-// the occupancy first): 16 service workgroups and 240 contraction workgroups.
-//   * Service workgroup m < M normalises residual row m as chunk_rmsnorm_rows_kernel<false> does
-//     (four waves, the same arithmetic through rms_row_values), writes it through and flags it;
-//     at the end it runs row m's post step as chunk_post_rows_kernel does (post_row).
+// the occupancy first): 240 contraction workgroups, then 16 service workgroups.
+//   * Service workgroup 240 + m (m < M) normalises residual row m as
+//     chunk_rmsnorm_rows_kernel<false> does (four waves, the same arithmetic through
+//     rms_row_values), writes it through and flags it; at the end it runs row m's post step as
+//     chunk_post_rows_kernel does (post_row), once one contraction workgroup's down flag and then
+//     all 240 carry the tag (a poll of one word per round until the end is near).
 //   * Contraction workgroup b issues its first up/gate weight loads, waits for the M row flags,
 //     stages the rows, and computes the GeGLU block b (L columns 64 b .. +64, all rows) as
 //     rows_kernel<GeGLU> does, then the down block (c, z) = (b % 60, b / 60) as rows_kernel<down>
@@ -416,6 +418,13 @@ __global__ __launch_bounds__((256 * RwShape<F, G>::NH)) void rows_kernel(FfnPara
 // hang, and the host takes the separate launches wherever the occupancy check fails. The service
 // workgroups' four upper waves end at once; their barriers then wait for the four that remain.
 //
+// Only calls that include the pre-norm take this kernel. Where the rows arrive normalised (the O ->
+// FFN rows path, whose O post rows write them), the separate launches measured faster: 39.8-40.0
+// against 40.2-40.4 us for O and the FFN at 16 MXFP4 rows. (The kernel with the post step on
+// leader contraction workgroups, 240 workgroups and no service ones, measured 30.3 us at 16 MXFP4
+// rows behind a pre-norm launch, 42.1 FP8; the service workgroups polling from the start were no
+// faster with longer sleeps between polls: 16 / 64 clocks x 64 cost 0.3 / 1.3 us.)
+//
 // Down steps per wave issued before p's quarter is staged (of 30 FP8, 15 FP4); the rest stream
 // behind the staging through the ring. Measured at 16 rows (graph-replayed): FP8 8 / 16 / 24 /
 // 30 steps 43.6 / 42.8 / 43.0 / 44.6 us; MXFP4 4 / 8 / 11 / 15 steps 31.4 / 30.6 / 30.7 / 31.7 us
@@ -439,8 +448,8 @@ __device__ __forceinline__ void rw_partial_publish(const f32x4& acc, float* yf, 
     }
 }
 
-constexpr int kRwService = kMaxDecodeM;                 // workgroups 0 .. 15: row m's pre-norm and post step
-constexpr int kRwFusedGrid = kRwService + kRwUpGroups;  // and 240 contraction workgroups
+constexpr int kRwService = kMaxDecodeM;                 // workgroups 240 + m: row m's pre-norm and post step
+constexpr int kRwFusedGrid = kRwUpGroups + kRwService;  // after the 240 contraction workgroups
 static_assert(kRwFusedGrid == kRowsEpochCounters * kRowsEpochPer, "equal workgroups per epoch counter");
 // flag words: the GeGLU blocks, the down blocks, the normalised rows
 constexpr int kRwFlagP = 0, kRwFlagDown = kRwUpGroups, kRwFlagNorm = 2 * kRwUpGroups;
@@ -465,10 +474,9 @@ __device__ __forceinline__ void rw_poll(const uint64_t* flags, int first, int n,
     }
 }
 
-// res: the M residual rows; x: their normalised rows, which the service workgroups write first when
-// norm is set (else they are there already).
+// res: the M residual rows; x: their normalised rows, which the service workgroups write.
 template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, bool norm, uint16_t* x, int M, uint16_t* y,
+__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, uint16_t* x, int M, uint16_t* y,
                                                                  float* yf, uint16_t* res, uint64_t* flags,
                                                                  uint32_t* tickets, uint32_t* err) {
     using TU = RwStream<F, true, kRwK, rw_ug_depth<F>()>;
@@ -484,12 +492,13 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, bo
     if (t == 0) ep_old = epoch_add(tickets + (kTicketRowsEpoch + blockIdx.x % kRowsEpochCounters) * kTicketStride);
 
     // ---- service workgroup m: the pre-norm of row m, then its post step (four waves)
-    if (blockIdx.x < kRwService) {
-        const int m = blockIdx.x;
+    const int b = blockIdx.x;
+    if (b >= kRwUpGroups) {
+        const int m = b - kRwUpGroups;
         if (m >= M || part != 0) return;
         float* red = reinterpret_cast<float*>(xs);
         const uint32_t tag = epoch_tag<kRowsEpochPer>(__shfl(ep_old, 0));
-        if (norm) {
+        {
             // chunk_rmsnorm_rows_kernel's arithmetic, its row written through (agent scope)
             const int c = min(t, kH / 16 - 1);
             const uint16_t* xr = res + (size_t)m * kH + c * 16;
@@ -509,7 +518,11 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, bo
             __syncthreads();
             if (t == 0) publish64(flags + kRwFlagNorm + m, tag);
         }
-        if (wave == 0) rw_poll(flags, kRwFlagDown, kRwUpGroups, tag, err, lane);
+        // first one contraction workgroup's down flag (one load per round), then all of them
+        if (wave == 0) {
+            rw_poll(flags, kRwFlagDown + m * (kRwUpGroups / kRwService), 1, tag, err, lane);
+            rw_poll(flags, kRwFlagDown, kRwUpGroups, tag, err, lane);
+        }
         __syncthreads();
         uint4 out[2];
         post_row<SK, F, kRwSplits>(yf, kRwSplits, M, F == FfnFormat::FP8 ? p.down_s : nullptr,
@@ -519,23 +532,17 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, bo
     }
 
     // ---- contraction workgroup b: up/gate (rows_kernel<GeGLU>)
-    const int b = blockIdx.x - kRwService;
     const uint32_t tag = epoch_tag<kRowsEpochPer>(__shfl(ep_old, 0));  // valid in wave 0
     f32x4 acc[2];
     {
         const int n0 = b * kRwGroupRows + tile * kRwTile;
-        RwRows<64 * NW> rows;
+        // the weights first; the rows once the service workgroups have published them
         TU st;
-        if (norm) {
-            // the weights first; the rows once the service workgroups have published them
-            rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, part * TU::KW, r, g);
-            if (wave == 0) rw_poll(flags, kRwFlagNorm, M, tag, err, lane);
-            rw_lds_barrier<-1>();
-            rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
-        } else {
-            rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
-            rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, part * TU::KW, r, g);
-        }
+        rw_prefetch<F, true, kRwK>(st, p.up, p.gate, p.up_s, p.gate_s, kH, n0, part * TU::KW, r, g);
+        if (wave == 0) rw_poll(flags, kRwFlagNorm, M, tag, err, lane);
+        rw_lds_barrier<-1>();
+        RwRows<64 * NW> rows;
+        rw_rows_load<64 * NW>(rows, x, kH, 0, M, t);
         rw_rows_store(rows, xs, t);
         rw_mma<F, true, kRwK>(st, xs, acc, part, r, g);
     }
@@ -618,8 +625,8 @@ bool rows_fused_fits(DevCtx* ctx) {
 // normed: the pre-norm's rows are already in ctx->hbuf (launch_o_ffn_rows)
 template <FfnFormat F, ScaleKind SK>
 hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed = false) {
-    if (rows_fused_fits<F, SK>(ctx)) {
-        hipLaunchKernelGGL((rows_fused_kernel<F, SK>), dim3(kRwFusedGrid), dim3(256 * kRwNH), 0, s, p, !normed, ctx->hbuf,
+    if (!normed && rows_fused_fits<F, SK>(ctx)) {
+        hipLaunchKernelGGL((rows_fused_kernel<F, SK>), dim3(kRwFusedGrid), dim3(256 * kRwNH), 0, s, p, ctx->hbuf,
                            M, ctx->pbuf, ctx->fbuf, p.residual + (size_t)m0 * kH, ctx->rows_flag, ctx->tickets, ctx->err);
         return hipGetLastError();
     }
