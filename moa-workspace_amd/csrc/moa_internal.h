@@ -201,7 +201,8 @@ hipError_t launch_post_pre_rows(const float* part, int splits, int M, const void
 hipError_t launch_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_o_rows(const OParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 // sliding_attention_output then decoder_feedforward on one residual for 2..kMaxDecodeM rows: O's post
-// rows also write the FFN's normalised input, so the FFN starts at its up/gate contraction.
+// rows also write the FFN's normalised input, so the FFN starts at its up/gate contraction (two
+// launches where the one-launch rows FFN fits: O's contraction, then the FFN with O's post rows).
 hipError_t launch_o_ffn_rows(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 hipError_t launch_full_qkv_rows(const QkvParams& p, int m0, int M, hipStream_t s, DevCtx* ctx);
 

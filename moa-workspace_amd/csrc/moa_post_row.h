@@ -48,11 +48,13 @@ __device__ __forceinline__ void rms_row_values(const float (&xv)[16], const floa
 // (shared/rmsnorm.rs:204-296, residual.rs:189-241; generate_references.py:411-413).
 // ZS: the most splits a call may have (the loads of all of them are in flight at once).
 // Row m; out[i] returns thread t's stored chunk t + 256 i (8 bf16 values) of the new residual.
+// rlds: the row's current residual in LDS (480 chunks of 8), read instead of res when given (a
+// caller that has just written the row itself).
 template <ScaleKind SK, FfnFormat F, int ZS>
 __device__ __forceinline__ void post_row(const float* __restrict__ part, int splits, int M, const void* scale,
                                          const float* __restrict__ gscale, const uint16_t* __restrict__ w_post,
                                          uint16_t* __restrict__ res, const uint16_t* __restrict__ ls, int m, float* red,
-                                         uint4 (&out)[2]) {
+                                         uint4 (&out)[2], const uint4* rlds = nullptr) {
     const int t = threadIdx.x;
     const float gs = F == FfnFormat::NVFP4 ? *gscale : 1.0f;
     constexpr int NC = kH / 8;  // 480 chunks of 8; thread t owns t and t + 256
@@ -63,7 +65,7 @@ __device__ __forceinline__ void post_row(const float* __restrict__ part, int spl
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = min(t + 256 * i, NC - 1);
-        rq[i] = ld16(res + (size_t)m * kH + c * 8);
+        rq[i] = rlds ? rlds[c] : ld16(res + (size_t)m * kH + c * 8);
         wq[i] = w_post ? ld16(w_post + c * 8) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll

@@ -474,9 +474,18 @@ __device__ __forceinline__ void rw_poll(const uint64_t* flags, int first, int n,
     }
 }
 
-// res: the M residual rows; x: their normalised rows, which the service workgroups write.
-template <FfnFormat F, ScaleKind SK>
-__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, uint16_t* x, int M, uint16_t* y,
+// O's post step ahead of the FFN (sliding_attention_output then decoder_feedforward on one
+// residual): O's split-K partial sums [4][M][H], its row scales and post-norm weight.
+struct RwOPost {
+    const float* part;
+    const void* scale;
+    const uint16_t* w_post;
+};
+
+// res: the M residual rows; x: their normalised rows, which the service workgroups write. OK: 0, or
+// O's scale kind + 1 when the service workgroups first apply O's post step to their row (o).
+template <FfnFormat F, ScaleKind SK, int OK = 0>
+__global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, RwOPost o, uint16_t* x, int M, uint16_t* y,
                                                                  float* yf, uint16_t* res, uint64_t* flags,
                                                                  uint32_t* tickets, uint32_t* err) {
     using TU = RwStream<F, true, kRwK, rw_ug_depth<F>()>;
@@ -499,14 +508,28 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, ui
         float* red = reinterpret_cast<float*>(xs);
         const uint32_t tag = epoch_tag<kRowsEpochPer>(__shfl(ep_old, 0));
         {
-            // chunk_rmsnorm_rows_kernel's arithmetic, its row written through (agent scope)
+            // chunk_rmsnorm_rows_kernel's arithmetic, its row written through (agent scope); with O's
+            // post step first, chunk_post_pre_rows_kernel's (the new residual row through LDS)
             const int c = min(t, kH / 16 - 1);
-            const uint16_t* xr = res + (size_t)m * kH + c * 16;
             float xv[16], wv[16];
-            bf16x8_to_f32(ld16(xr), xv);
-            bf16x8_to_f32(ld16(xr + 8), xv + 8);
             bf16x8_to_f32(ld16(p.pre_rms + c * 16), wv);
             bf16x8_to_f32(ld16(p.pre_rms + c * 16 + 8), wv + 8);
+            if constexpr (OK != 0) {
+                uint4 out[2];
+                post_row<OK == 1 ? ScaleKind::F32 : ScaleKind::BF16, FfnFormat::FP8, kRwSplits>(
+                    o.part, kRwSplits, M, o.scale, nullptr, o.w_post, res, nullptr, m, red, out);
+                uint4* row = xs + 64;  // past red; kept until the post step below
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    if (t + 256 * i < kH / 8) row[t + 256 * i] = out[i];
+                __syncthreads();
+                bf16x8_to_f32(row[2 * c], xv);
+                bf16x8_to_f32(row[2 * c + 1], xv + 8);
+            } else {
+                const uint16_t* xr = res + (size_t)m * kH + c * 16;
+                bf16x8_to_f32(ld16(xr), xv);
+                bf16x8_to_f32(ld16(xr + 8), xv + 8);
+            }
             uint32_t h[8];
             rms_row_values(xv, wv, red, h);
             if (t < kH / 16) {
@@ -524,10 +547,11 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, ui
             rw_poll(flags, kRwFlagDown, kRwUpGroups, tag, err, lane);
         }
         __syncthreads();
+        // with O's post step first, row m's residual is the one in LDS (this workgroup wrote it)
         uint4 out[2];
         post_row<SK, F, kRwSplits>(yf, kRwSplits, M, F == FfnFormat::FP8 ? p.down_s : nullptr,
                                    F == FfnFormat::NVFP4 ? p.down_g : nullptr, p.post_rms, res, p.layer_scalar, m, red,
-                                   out);
+                                   out, OK != 0 ? xs + 64 : nullptr);
         return;
     }
 
@@ -622,14 +646,18 @@ bool rows_fused_fits(DevCtx* ctx) {
     return known == 1;
 }
 
+// One launch of rows_fused_kernel for rows m0 .. m0 + M - 1 (with O's post step first when OK != 0).
+template <FfnFormat F, ScaleKind SK, int OK>
+hipError_t launch_rows_fused(const FfnParams& p, const RwOPost& o, int m0, int M, hipStream_t s, DevCtx* ctx) {
+    hipLaunchKernelGGL((rows_fused_kernel<F, SK, OK>), dim3(kRwFusedGrid), dim3(256 * kRwNH), 0, s, p, o, ctx->hbuf, M,
+                       ctx->pbuf, ctx->fbuf, p.residual + (size_t)m0 * kH, ctx->rows_flag, ctx->tickets, ctx->err);
+    return hipGetLastError();
+}
+
 // normed: the pre-norm's rows are already in ctx->hbuf (launch_o_ffn_rows)
 template <FfnFormat F, ScaleKind SK>
 hipError_t rows_ffn_impl(const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx, bool normed = false) {
-    if (!normed && rows_fused_fits<F, SK>(ctx)) {
-        hipLaunchKernelGGL((rows_fused_kernel<F, SK>), dim3(kRwFusedGrid), dim3(256 * kRwNH), 0, s, p, ctx->hbuf,
-                           M, ctx->pbuf, ctx->fbuf, p.residual + (size_t)m0 * kH, ctx->rows_flag, ctx->tickets, ctx->err);
-        return hipGetLastError();
-    }
+    if (!normed && rows_fused_fits<F, SK>(ctx)) return launch_rows_fused<F, SK, 0>(p, RwOPost{}, m0, M, s, ctx);
     hipError_t e = normed ? hipSuccess : launch_rmsnorm_rows(p.residual + (size_t)m0 * kH, p.pre_rms, ctx->hbuf, M, s);
     if (e != hipSuccess) return e;
     e = rw_launch<F, SK, true>(dim3(kRwUpGroups, 1, 1), s, p, ctx->hbuf, kH, M, ctx->pbuf, nullptr);
@@ -824,18 +852,45 @@ hipError_t launch_ffn_rows(const FfnParams& p, int m0, int M, hipStream_t s, Dev
     return ffn_rows_dispatch(p, m0, M, s, ctx, false);
 }
 
-// O's contraction as launch_o_rows runs it, then one row kernel for O's post rows and the FFN's
-// pre-norm (the bits of chunk_post_rows_kernel, then of chunk_rmsnorm_rows_kernel<false>), then the
-// FFN's rows path from its up/gate contraction on.
+// O's contraction as launch_o_rows runs it, then O's post rows and the FFN's pre-norm (the bits of
+// chunk_post_rows_kernel, then of chunk_rmsnorm_rows_kernel<false>) and the FFN: in one launch on
+// rows_fused_kernel's service workgroups where its grid fits, else as one row kernel
+// (chunk_post_pre_rows_kernel) and the FFN's rows path from its up/gate contraction on.
+static_assert(kQs / kRwOKR == kRwSplits, "O's split-K partial sums: as many as the down projection's");
+
+// O's post step and the FFN in one launch (rows_fused_kernel with O's post on its service
+// workgroups), for the formats and O scale kinds the fused kernel is instantiated for.
+template <FfnFormat F, ScaleKind SK>
+static bool o_ffn_rows_fused(const OParams& o, const FfnParams& p, const float* opart, int m0, int M, hipStream_t s,
+                             DevCtx* ctx, hipError_t* e) {
+    if (!rows_fused_fits<F, SK>(ctx)) return false;
+    const RwOPost op{opart, o.os, o.post_rms};
+    *e = o.scale_kind == ScaleKind::F32 ? launch_rows_fused<F, SK, 1>(p, op, m0, M, s, ctx)
+                                        : launch_rows_fused<F, SK, 2>(p, op, m0, M, s, ctx);
+    return true;
+}
+
 hipError_t launch_o_ffn_rows(const OParams& o, const FfnParams& p, int m0, int M, hipStream_t s, DevCtx* ctx) {
     if (M < 1 || M > kMaxDecodeM || o.div || o.residual != p.residual) return hipErrorInvalidValue;
     ProjRows a{};
     a.x = o.x + (size_t)m0 * kQs; a.M = M; a.K = kQs; a.N = kH;
     a.w[0] = o.ow; a.nseg[0] = 0; a.nseg[1] = kH; a.nsegs = 1;
-    a.yf = ctx->fbuf;
+    // O's partial sums past the FFN's own (the one launch reads the first while it writes the second)
+    float* opart = ctx->fbuf + (size_t)kRwSplits * kMaxDecodeM * kH;
+    a.yf = opart;
     hipError_t e = rw_proj<kRwOKR>(a, s);
     if (e != hipSuccess) return e;
-    e = launch_post_pre_rows(ctx->fbuf, kQs / kRwOKR, M, o.os, o.scale_kind, o.post_rms, o.residual + (size_t)m0 * kH,
+    bool done = false;
+    switch (p.fmt) {
+        case FfnFormat::FP8:
+            done = p.scale_kind == ScaleKind::F32 ? o_ffn_rows_fused<FfnFormat::FP8, ScaleKind::F32>(o, p, opart, m0, M, s, ctx, &e)
+                                                  : o_ffn_rows_fused<FfnFormat::FP8, ScaleKind::BF16>(o, p, opart, m0, M, s, ctx, &e);
+            break;
+        case FfnFormat::NVFP4: done = o_ffn_rows_fused<FfnFormat::NVFP4, ScaleKind::F32>(o, p, opart, m0, M, s, ctx, &e); break;
+        case FfnFormat::MXFP4: done = o_ffn_rows_fused<FfnFormat::MXFP4, ScaleKind::F32>(o, p, opart, m0, M, s, ctx, &e); break;
+    }
+    if (done) return e;
+    e = launch_post_pre_rows(opart, kQs / kRwOKR, M, o.os, o.scale_kind, o.post_rms, o.residual + (size_t)m0 * kH,
                              p.pre_rms, ctx->hbuf, s);
     if (e != hipSuccess) return e;
     return ffn_rows_dispatch(p, m0, M, s, ctx, true);
