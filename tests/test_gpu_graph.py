@@ -129,3 +129,72 @@ def test_graph_replays_of_the_next_row_operators_match_eager():
         for w, t, name in zip(want, outs, names):
             assert np.array_equal(w, host(t)), f"replay {replay}: {name} differs from the eager result"
     assert ops.device_errors() == 0
+
+
+def test_graph_replays_of_the_16_row_operators_match_eager():
+    """16 token rows: the one-launch rows FFN (MXFP4 and FP8: pre-norm, contractions and post step
+    in one kernel with tagged flags), O then the FFN through one entry point (O's post rows on the
+    FFN kernel's service workgroups), and the rows-path QKV and O, captured in one graph: every
+    replay gives the eager bits (the hand-off tags come from device-side epoch counters, so a
+    replayed launch never meets a flag of an earlier replay)."""
+    need_gpu()
+    from moa_amd import ops
+    ops.init(0)
+    mx = synth.cfg_ffn_mxfp4(4)
+    f = synth.cfg_ffn_fp8(4)
+    o = synth.cfg_o(4, M=16)
+    q = synth.cfg_qkv(4, M=16, pos=600)
+    MXK = ("up_weight_packed", "gate_weight_packed", "down_weight_packed", "up_weight_scale", "gate_weight_scale",
+           "down_weight_scale")
+    FK = ("up_weight", "gate_weight", "down_weight", "up_weight_scale", "gate_weight_scale", "down_weight_scale")
+    M_ = {k: dev(mx[k]) for k in MXK}
+    F_ = {k: dev(f[k]) for k in FK}
+    pre, post, ls = (dev(f[k]) for k in ("pre_ff_rms_weight", "post_ff_rms_weight", "layer_scalar"))
+    O_ = {k: dev(o[k]) for k in ("x", "o_weight", "o_weight_scale", "post_attn_rms_weight")}
+    Q_ = {k: dev(q[k]) for k in ("x", "q_weight", "k_weight", "v_weight", "q_weight_scale", "k_weight_scale",
+                                 "v_weight_scale", "input_rms_weight", "q_rms_weight", "k_rms_weight", "cos", "sin")}
+    kv = torch.tensor([q["kv_offset"]], dtype=torch.int32, device="cuda")
+    ro = torch.tensor([q["rope_offset"]], dtype=torch.int32, device="cuda")
+    kc0, vc0 = dev(q["k_cache"]), dev(q["v_cache"])
+    kc, vc = kc0.clone(), vc0.clone()
+    q_out = torch.zeros(16 * 4096, dtype=torch.int16, device="cuda")
+    r0 = dev(synth.bf16_normal("graph16.residual", (16, 3840)))
+    r_mx, r_f8, r_of, r_o = r0.clone(), r0.clone(), r0.clone(), r0.clone()
+
+    def step():
+        for t in (r_mx, r_f8, r_of, r_o):
+            t.copy_(r0)
+        kc.copy_(kc0)
+        vc.copy_(vc0)
+        ops.decoder_feedforward_mxfp4(r_mx, pre, *[M_[k] for k in MXK], post, ls)
+        ops.decoder_feedforward_fp8(r_f8, pre, *[F_[k] for k in FK], post, ls)
+        ops.sliding_attention_output_feedforward_mxfp4(O_["x"], O_["post_attn_rms_weight"], O_["o_weight"],
+                                                       O_["o_weight_scale"], r_of, pre, *[M_[k] for k in MXK], post,
+                                                       ls)
+        ops.sliding_attention_output(O_["x"], O_["post_attn_rms_weight"], O_["o_weight"], O_["o_weight_scale"], r_o)
+        ops.sliding_project_qkv(Q_["x"], Q_["q_weight"], Q_["k_weight"], Q_["v_weight"], Q_["q_weight_scale"],
+                                Q_["k_weight_scale"], Q_["v_weight_scale"], Q_["input_rms_weight"],
+                                Q_["q_rms_weight"], Q_["k_rms_weight"], kv, ro, Q_["cos"], Q_["sin"], kc, vc, q_out)
+
+    outs = (r_mx, r_f8, r_of, r_o, kc, vc, q_out)
+    names = ("ffn mxfp4", "ffn fp8", "o -> ffn", "o", "k_cache", "v_cache", "q_out")
+    step()
+    torch.cuda.synchronize()
+    assert ops.device_errors() == 0
+    want = [host(t).copy() for t in outs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for replay in range(3):
+        say(f"16-row graph replay {replay}")
+        for t in (r_mx, r_f8, r_of, q_out):
+            t.fill_(0)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for w, t, name in zip(want, outs, names):
+            assert np.array_equal(w, host(t)), f"replay {replay}: {name} differs from the eager result"
+        step()  # eager again
+        torch.cuda.synchronize()
+        assert np.array_equal(host(r_mx), want[0])
+    assert ops.device_errors() == 0
