@@ -533,9 +533,9 @@ __global__ __launch_bounds__(256 * kRwNH) void rows_fused_kernel(FfnParams p, Rw
             uint32_t h[8];
             rms_row_values(xv, wv, red, h);
             if (t < kH / 16) {
-                uint64_t* o = reinterpret_cast<uint64_t*>(x + (size_t)m * kH + c * 16);
+                uint64_t* dst = reinterpret_cast<uint64_t*>(x + (size_t)m * kH + c * 16);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) publish64(o + i, ((uint64_t)h[2 * i + 1] << 32) | h[2 * i]);
+                for (int i = 0; i < 4; ++i) publish64(dst + i, ((uint64_t)h[2 * i + 1] << 32) | h[2 * i]);
             }
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
