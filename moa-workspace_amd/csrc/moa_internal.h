@@ -95,7 +95,8 @@ struct DevCtx {
     int8_t qkv_fused[2] = {-1, -1};                  // per scale kind
     int8_t full_o_fused[2] = {-1, -1};               // the same for full_attention_output
     int8_t o_ffn_fused[3] = {-1, -1, -1};            // the single-launch O -> FFN, per FFN format
-    int8_t rows_fused[6] = {-1, -1, -1, -1, -1, -1}; // the one-launch rows FFN, per (format, scale kind)
+    int8_t rows_fused[18] = {-1, -1, -1, -1, -1, -1, -1, -1, -1,  // the one-launch rows FFN, per (format,
+                             -1, -1, -1, -1, -1, -1, -1, -1, -1}; // scale kind, O post step kind)
 };
 
 // Returns the context of the current device, allocating it on first use. nullptr on failure.

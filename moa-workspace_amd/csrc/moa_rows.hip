@@ -631,16 +631,16 @@ hipError_t rw_launch(dim3 grid, hipStream_t s, const FfnParams& p, const uint16_
 
 std::atomic<int> g_rows_one_launch{1};
 
-// Whether rows_fused_kernel runs: its hand-off words exist, tests have not switched it off, and its
-// grid fits on the device at once (checked once per device and format).
-template <FfnFormat F, ScaleKind SK>
+// Whether rows_fused_kernel<F, SK, OK> runs: its hand-off words exist, tests have not switched it
+// off, and its grid fits on the device at once (checked once per device and instantiation).
+template <FfnFormat F, ScaleKind SK, int OK = 0>
 bool rows_fused_fits(DevCtx* ctx) {
     if (!ctx->rows_flag || !g_rows_one_launch.load()) return false;
-    int8_t& known = ctx->rows_fused[(int)F * 2 + (int)SK];
+    int8_t& known = ctx->rows_fused[((int)F * 2 + (int)SK) * 3 + OK];
     if (known < 0) {
         int per_cu = 0;
         const hipError_t e =
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rows_fused_kernel<F, SK>, 256 * kRwNH, 0);
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rows_fused_kernel<F, SK, OK>, 256 * kRwNH, 0);
         known = (e == hipSuccess && per_cu * ctx->cus >= kRwFusedGrid) ? 1 : 0;
     }
     return known == 1;
@@ -863,10 +863,14 @@ static_assert(kQs / kRwOKR == kRwSplits, "O's split-K partial sums: as many as t
 template <FfnFormat F, ScaleKind SK>
 static bool o_ffn_rows_fused(const OParams& o, const FfnParams& p, const float* opart, int m0, int M, hipStream_t s,
                              DevCtx* ctx, hipError_t* e) {
-    if (!rows_fused_fits<F, SK>(ctx)) return false;
     const RwOPost op{opart, o.os, o.post_rms};
-    *e = o.scale_kind == ScaleKind::F32 ? launch_rows_fused<F, SK, 1>(p, op, m0, M, s, ctx)
-                                        : launch_rows_fused<F, SK, 2>(p, op, m0, M, s, ctx);
+    if (o.scale_kind == ScaleKind::F32) {
+        if (!rows_fused_fits<F, SK, 1>(ctx)) return false;
+        *e = launch_rows_fused<F, SK, 1>(p, op, m0, M, s, ctx);
+    } else {
+        if (!rows_fused_fits<F, SK, 2>(ctx)) return false;
+        *e = launch_rows_fused<F, SK, 2>(p, op, m0, M, s, ctx);
+    }
     return true;
 }
 
