@@ -68,8 +68,10 @@ BYTES = {"ffn": 177_116_176, "o": 15_775_232, "qkv": 31_523_848,
          # reciprocal global scales) on its run-0 inputs, M = 1
          "ffn_nvfp4": 3 * 29_491_200 + 3 * 3_686_400 + 3 * 4 + 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
          "ffn_mxfp4_m16": 94_003_200 + 16 * 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
-         # the FP8 FFN at 16 rows: the M = 1 bytes plus 15 more residual rows read and written
+         # the FP8 FFN at 16 rows: the M = 1 bytes plus 15 more residual rows read and written; the
+         # same for the reference's NVFP4 operand types
          "ffn_m16": 177_116_176 + 15 * 2 * 3840 * 2,
+         "ffn_nvfp4_m16": 3 * 29_491_200 + 3 * 3_686_400 + 3 * 4 + 16 * 2 * 3840 * 2 + 2 * 3840 * 2 + 16,
          # O at 16 rows (15 more input rows and residual rows read and written), and O then the
          # MXFP4 FFN on those 16 residual rows through one entry point (less the rows between them)
          "o_m16": 15_775_232 + 15 * (4096 * 2 + 2 * 3840 * 2),
@@ -115,7 +117,7 @@ def main() -> int:
     ap.add_argument("--chunk-rows", type=int, default=256,
                     help="rows of the config-4 layer chunk measured after the decode step (0 = skip)")
     ap.add_argument("--profile", choices=("ffn", "o", "qkv", "attn", "logits", "fqkv", "fattn", "fattn_fused", "fattn_fused64", "fo",
-                                          "ffn_mxfp4", "ffn_mxfp4_m16", "ffn_m16", "ffn_nvfp4", "o_ffn", "o_m16", "o_ffn_mxfp4_m16",
+                                          "ffn_mxfp4", "ffn_mxfp4_m16", "ffn_m16", "ffn_nvfp4", "ffn_nvfp4_m16", "o_ffn", "o_m16", "o_ffn_mxfp4_m16",
                                           "chunk", "chunk_o_ffn", "floor"), default=None,
                     help="run one operator (or the config-4 layer chunk) host-driven for a counter profile, "
                          "then a 256 MiB copy")
@@ -290,6 +292,10 @@ def main() -> int:
     def run_ffn_mxfp4_m16(i):
         run_ffn_mxfp4(i, mx_res16)
 
+    def run_ffn_nvfp4_m16(i):
+        w = NVW[i % nnv]
+        ops.decoder_feedforward(mx_res16, nv_pre, *[w[k] for k in NVK], nv_post, nv_ls)
+
     def run_ffn_m16(i):
         w = FW[i % nf]
         ops.decoder_feedforward_fp8(mx_res16, f_pre, w["up_weight"], w["gate_weight"], w["down_weight"],
@@ -428,7 +434,8 @@ def main() -> int:
         fn = {"ffn": run_ffn, "o": run_o, "qkv": run_qkv, "attn": run_attn, "logits": run_logits,
               "fqkv": run_fqkv, "fattn": run_fattn, "fattn_fused": run_fattn_fused,
               "fattn_fused64": run_fattn_fused64, "fo": run_fo, "ffn_mxfp4": run_ffn_mxfp4,
-              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "ffn_m16": run_ffn_m16, "chunk": run_layer,
+              "ffn_mxfp4_m16": run_ffn_mxfp4_m16, "ffn_m16": run_ffn_m16, "ffn_nvfp4_m16": run_ffn_nvfp4_m16,
+              "chunk": run_layer,
               "chunk_o_ffn": run_layer_o_ffn,
               "o_ffn": run_o_ffn, "o_m16": run_o_m16, "o_ffn_mxfp4_m16": run_o_ffn_mxfp4_m16,
               "ffn_nvfp4": run_ffn_nvfp4}[args.profile]
@@ -448,6 +455,7 @@ def main() -> int:
     per_op = {}
     for name, fn in (("qkv", run_qkv), ("o", run_o), ("ffn", run_ffn), ("o_ffn", run_o_ffn), ("ffn_mxfp4", run_ffn_mxfp4),
                      ("ffn_mxfp4_m16", run_ffn_mxfp4_m16), ("ffn_m16", run_ffn_m16), ("ffn_nvfp4", run_ffn_nvfp4),
+                     ("ffn_nvfp4_m16", run_ffn_nvfp4_m16),
                      ("o_m16", run_o_m16),
                      ("o_ffn_mxfp4_m16", run_o_ffn_mxfp4_m16),
                      ("attn", run_attn), ("logits", run_logits),
